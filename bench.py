@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""Benchmark: one rank's share of exact causal ring attention, forward +
+recompute backward, on one MI355X (BASELINE configs 2 and 3).
+
+Workload (one "step"): rank 7 of an 8-rank ring, a 32768-token bf16 local
+query shard, Hq = Hkv = 16, d = 128.  Forward: the diagonal KV shard plus 7
+preceding full KV shards, each hop's partial merged by log-sum-exp into the
+running state (fwd kernel + merge kernel per hop).  Backward: preprocess
+(delta, LSE), then per hop the dQ kernel (accumulating dQ across shards) and
+the dK/dV kernel (per-shard dK/dV, as they would travel back around the
+ring).  Inputs (Q, K, V, dO ~ N(0,1), seeded) are resident in HBM before the
+timed region.
+
+FLOP convention (algorithmic, fully masked tiles not counted): a full
+(query shard x KV shard) forward is 4*Nq*Nk*H*d, the diagonal counts half,
+the backward is 2.5x the forward.  Peak: bf16 dense MFMA 2516.6 TFLOP/s.
+
+The CPU baseline times the C restatement of the reference algorithm
+(oracle/ring_ref.c, OpenMP on the host cores) on a bounded sample: one head
+of the same geometry with a shorter shard, sized to ~15 s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6
+METRIC = "causal attn fwd+bwd TFLOP/s @32k bf16 shard, % MFMA peak; vs CPU ref"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=32768, help="local shard tokens")
+    ap.add_argument("--world", type=int, default=8)
+    ap.add_argument("--rank", type=int, default=7)
+    ap.add_argument("--heads", type=int, default=16)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target duration of the CPU-baseline sample (0 disables it)")
+    return ap.parse_args()
+
+
+def cpu_baseline(args, target_s: float):
+    """Times the C oracle (the reference's blocked fp32 algorithm) on one head
+    of the bench geometry with a shard of n_s tokens, n_s sized so the run
+    takes about target_s seconds."""
+    import numpy as np
+
+    from oracle import ring as oring
+
+    world, rank, d = args.world, args.rank, args.head_dim
+
+    def run(ns):
+        rng = np.random.default_rng(99)
+        mk = lambda: rng.standard_normal((1, ns, 1, d)).astype(np.float32)  # noqa: E731
+        qs = [mk() for _ in range(world)]
+        ks = [mk() for _ in range(world)]
+        vs = [mk() for _ in range(world)]
+        go = mk()
+        t0 = time.perf_counter()
+        out, m, l = oring.ring_fwd_with_stats(qs, ks, vs, rank)
+        # other ranks' (out, m, l, dO) only enter pass-1 hops whose pairs are
+        # all masked for this rank; any finite values give zero there
+        outs = [np.zeros_like(out) for _ in range(world)]
+        ms = [np.zeros_like(m) for _ in range(world)]
+        ls = [np.ones_like(l) for _ in range(world)]
+        gos = [np.zeros_like(go) for _ in range(world)]
+        outs[rank], ms[rank], ls[rank], gos[rank] = out, m, l, go
+        oring.ring_bwd(qs, ks, vs, outs, ms, ls, gos, rank)
+        return time.perf_counter() - t0
+
+    ns = 256
+    t = run(ns)
+    while t < target_s / 8 and ns < args.tokens:
+        ns = min(args.tokens, ns * 2)
+        t = run(ns)
+    if t < target_s * 0.6 and ns < args.tokens:
+        ns = min(args.tokens, int(ns * math.sqrt(target_s / t)) // 128 * 128)
+        t = run(ns)
+    hops_full = rank  # owners rank-1 .. 0 are full, owner rank is the diagonal
+    fwd = 4.0 * ns * ns * 1 * d * (hops_full + 0.5)
+    flops = 3.5 * fwd
+    return {
+        "value": round(flops / t / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": oring.num_threads(),
+        "kind": "port",
+        "sample": (f"C restatement of the reference algorithm (fp32, block_q=64, block_k=128, "
+                   f"two-pass backward), 1 of {args.heads} heads, world {world} rank {rank}, "
+                   f"{ns}-token shards, d={d}: fwd+bwd {flops / 1e9:.1f} GFLOP in {t:.2f} s"),
+        "seconds": round(t, 3),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's share of the ring; --gpus {args.gpus} is not "
+              f"supported (this build runs on one GPU only)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from longctx100m_amd import ring_attention as ra
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    n, h, d, world, rank = args.tokens, args.heads, args.head_dim, args.world, args.rank
+    bf = torch.bfloat16
+    log(f"setup: world={world} rank={rank} n={n} H={h} d={d} bf16")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    randn = lambda *s: torch.randn(*s, generator=gen, device=dev, dtype=torch.float32).to(bf)  # noqa: E731
+    q = randn(1, n, h, d)
+    dout = randn(1, n, h, d)
+    ks = [randn(1, n, h, d) for _ in range(world)]
+    vs = [randn(1, n, h, d) for _ in range(world)]
+    q_pos0 = rank * n
+    owners = [(rank - hop) % world for hop in range(world)]
+    owners = [b for b in owners if b * n <= q_pos0 + n - 1]  # fully masked hops skipped
+
+    f32 = dict(device=dev, dtype=torch.float32)
+    o_run = torch.empty(1, n, h, d, **f32)
+    m = torch.empty(1, h, n, **f32)
+    l = torch.empty(1, h, n, **f32)
+    o_part = torch.empty_like(o_run)
+    m_part = torch.empty_like(m)
+    l_part = torch.empty_like(l)
+    out = torch.empty(1, n, h, d, device=dev, dtype=bf)
+    delta = torch.empty_like(m)
+    lse2 = torch.empty_like(m)
+    dq_acc = torch.empty(1, n, h, d, **f32)
+    dk_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
+    dv_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
+
+    timers = {}
+
+    def timed(name, fn):
+        if timers is None or name is None:
+            fn()
+            return
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        timers.setdefault(name, []).append((s, e))
+
+    def step(record: bool):
+        nonlocal timers
+        saved = timers
+        if not record:
+            timers = None
+        for i, b in enumerate(owners):
+            tag = "diag" if b == rank else "full"
+            if i == 0:
+                timed(f"fwd_{tag}", lambda b=b: ra.fwd_shard(q, ks[b], vs[b], q_pos0=q_pos0,
+                                                             k_pos0=b * n, o=o_run, m=m, l=l))
+            else:
+                timed(f"fwd_{tag}", lambda b=b: ra.fwd_shard(q, ks[b], vs[b], q_pos0=q_pos0,
+                                                             k_pos0=b * n, o=o_part, m=m_part,
+                                                             l=l_part))
+                last = i + 1 == len(owners)
+                timed("merge", lambda last=last: ra.merge(o_run, m, l, o_part, m_part, l_part,
+                                                          out=out if last else None))
+        if len(owners) == 1:
+            ra.cast(o_run, out)
+        timed("bwd_preprocess", lambda: ra.bwd_preprocess(out, dout, m, l, delta, lse2))
+        dq_acc.zero_()
+        for b in owners:
+            dk_acc[b].zero_()
+            dv_acc[b].zero_()
+        for b in owners:
+            tag = "diag" if b == rank else "full"
+            timed(f"dq_{tag}", lambda b=b: ra.bwd_shard(q, ks[b], vs[b], dout, lse2, delta,
+                                                        q_pos0=q_pos0, k_pos0=b * n,
+                                                        dq_acc=dq_acc))
+            timed(f"dkdv_{tag}", lambda b=b: ra.bwd_shard(q, ks[b], vs[b], dout, lse2, delta,
+                                                          q_pos0=q_pos0, k_pos0=b * n,
+                                                          dk_acc=dk_acc[b], dv_acc=dv_acc[b]))
+        timers = saved
+
+    for i in range(args.warmup):
+        step(False)
+        torch.cuda.synchronize()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t_start.record()
+    for i in range(args.steps):
+        step(True)
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_total = t_start.elapsed_time(t_end)
+    ms_per_step = ms_total / args.steps
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall:.2f} s)")
+
+    kern = {}
+    for name, evs in timers.items():
+        durs = [s.elapsed_time(e) for s, e in evs]
+        kern[name] = {"launches_per_step": len(durs) // args.steps,
+                      "avg_ms": round(sum(durs) / len(durs), 4)}
+
+    n_full = sum(1 for b in owners if b != rank)
+    has_diag = rank in owners
+    unit = 4.0 * n * n * h * d  # forward flops of one full (Q shard x KV shard) pair
+    fwd_flops = unit * (n_full + (0.5 if has_diag else 0.0))
+    total_flops = 3.5 * fwd_flops
+    tflops = total_flops / (ms_per_step * 1e-3) / 1e12
+
+    # Dominant kernel class by time per step; roofline against the bf16 MFMA peak.
+    tot = {k: v["avg_ms"] * v["launches_per_step"] for k, v in kern.items()}
+    fwd_t = tot.get("fwd_full", 0.0) + tot.get("fwd_diag", 0.0)
+    bwd_t = sum(tot.get(k, 0.0) for k in ("dq_full", "dq_diag", "dkdv_full", "dkdv_diag"))
+    if n_full > 0 and bwd_t >= fwd_t:
+        pair_ms = kern["dq_full"]["avg_ms"] + kern["dkdv_full"]["avg_ms"]
+        achieved = 2.5 * unit / (pair_ms * 1e-3) / 1e12
+        rl_kernel = "bwd_dq_kernel<128> + bwd_dkdv_kernel<128> (one full hop)"
+        rl_units = f"2.5 x 4*N*N*H*d = {2.5 * unit / 1e12:.3f} TFLOP per full hop"
+    elif n_full > 0:
+        achieved = unit / (kern["fwd_full"]["avg_ms"] * 1e-3) / 1e12
+        rl_kernel = "fwd_mfma_kernel<128> (one full hop)"
+        rl_units = f"4*N*N*H*d = {unit / 1e12:.3f} TFLOP per full hop"
+    else:
+        achieved = tflops
+        rl_kernel = "whole step"
+        rl_units = f"{total_flops / 1e12:.3f} TFLOP per step"
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": None, "kernel": rl_kernel, "algorithmic": rl_units}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("cpu baseline (C restatement of the reference algorithm) ...")
+        cpu = cpu_baseline(args, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['seconds']} s)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q, K, V, dO ~ N(0,1) (seeded torch generator), resident in HBM",
+        "config": {
+            "workload": (f"BASELINE configs 2+3: rank {rank} of {world}, {n}-token bf16 local "
+                         f"shard, Hq=Hkv={h}, d={d}; fwd over diagonal + {n_full} full KV shards "
+                         f"with LSE merge, then recompute bwd (dQ across shards, dK/dV per "
+                         f"shard)"),
+            "world": world, "rank": rank, "local_tokens": n, "heads_q": h, "heads_kv": h,
+            "head_dim": d, "parallelism": "one rank's share on one GPU (ring emulated in HBM)",
+        },
+        "pct_mfma_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "flops_per_step": total_flops,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kern,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

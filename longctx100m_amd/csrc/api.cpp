@@ -1,0 +1,549 @@
+// C-ABI entry points of liblongctx100m_attn (declared in include/longctx100m_attn.h).
+//
+// Host-side mirror of the reference's ring-attention module
+// (rust/longctx100m-model/src/ring_attention.rs): argument validation with
+// the reference's messages (rs:148-171), the in-process ring emulation over
+// KV shards held in HBM (hop h visits owner (rank - h) mod world, rs:191-225),
+// the two-pass backward (rs:367-460) and the host-pointer forms a CPU-tensor
+// caller binds.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "../../include/longctx100m_attn.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_error(hipError_t e, const char* where) {
+  return set_error(LC_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define LC_TRY_HIP(expr, where)                \
+  do {                                         \
+    hipError_t e_ = (expr);                    \
+    if (e_ != hipSuccess) return hip_error(e_, where); \
+  } while (0)
+
+size_t dtype_size(int dtype) { return dtype == LC_DTYPE_BF16 ? 2 : 4; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks common to every shape: mirrors the reference's shape errors.
+int check_shape(const lc_attn_shape_t* s) {
+  if (s == nullptr) return set_error(LC_ERR_INVALID, "null shape argument");
+  if (s->batch <= 0 || s->heads_q <= 0 || s->heads_kv <= 0 || s->head_dim <= 0 ||
+      s->q_tokens < 0 || s->kv_tokens < 0)
+    return set_error(LC_ERR_INVALID, "q, k, v must have shape [batch, tokens, heads, head_dim]");
+  if (s->heads_q % s->heads_kv != 0)
+    return set_error(LC_ERR_INVALID, "heads_q (%d) must be a multiple of heads_kv (%d)",
+                     s->heads_q, s->heads_kv);
+  if (s->dtype != LC_DTYPE_F32 && s->dtype != LC_DTYPE_BF16)
+    return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", s->dtype);
+  if (s->head_dim > 256)
+    return set_error(LC_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", s->head_dim);
+  return LC_OK;
+}
+
+lc::Problem make_problem(const lc_attn_shape_t* s, const lc_attn_mask_t* m) {
+  lc::Problem p;
+  p.B = s->batch;
+  p.Nq = s->q_tokens;
+  p.Nk = s->kv_tokens;
+  p.Hq = s->heads_q;
+  p.Hkv = s->heads_kv;
+  p.D = s->head_dim;
+  p.dtype = s->dtype;
+  p.precise = (s->flags & LC_FLAG_PRECISE) != 0;
+  p.q_pos0 = m ? m->q_pos0 : 0;
+  p.k_pos0 = m ? m->k_pos0 : 0;
+  p.valid = (m && m->valid_length >= 0) ? m->valid_length : std::numeric_limits<int64_t>::max();
+  p.causal = m ? m->causal != 0 : true;
+  p.scale = static_cast<float>(std::pow(static_cast<double>(p.D), -0.5));
+  return p;
+}
+
+bool use_mfma(const lc::Problem& p, const void* q, const void* k, const void* v,
+              const void* dout) {
+  return lc::mfma_supported(p) && aligned16(q) && aligned16(k) && aligned16(v) &&
+         (dout == nullptr || aligned16(dout));
+}
+
+// Whether any (query, key) pair of the shard pair is unmasked.
+bool pair_active(const lc::Problem& p) {
+  if (p.Nq == 0 || p.Nk == 0) return false;
+  return lc::key_end_for(p, p.Nq) > 0;
+}
+
+int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v, float* o,
+              float* m, float* l, hipStream_t st) {
+  hipError_t e;
+  if (use_mfma(p, q, k, v, nullptr))
+    e = lc::launch_fwd_mfma(p, q, k, v, o, m, l, st);
+  else
+    e = lc::launch_fwd_generic(p, q, k, v, o, m, l, st);
+  if (e != hipSuccess) return hip_error(e, "lc_attn_fwd_shard launch");
+  return LC_OK;
+}
+
+int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v, const void* dout,
+              const float* lse2, const float* delta, float* dq, float* dk, float* dv,
+              hipStream_t st) {
+  const bool mf = use_mfma(p, q, k, v, dout);
+  if (dq != nullptr) {
+    hipError_t e = mf ? lc::launch_bwd_dq_mfma(p, q, k, v, dout, lse2, delta, dq, st)
+                      : lc::launch_bwd_dq_generic(p, q, k, v, dout, lse2, delta, dq, st);
+    if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dq launch");
+  }
+  if (dk != nullptr) {
+    hipError_t e = mf ? lc::launch_bwd_dkdv_mfma(p, q, k, v, dout, lse2, delta, dk, dv, st)
+                      : lc::launch_bwd_dkdv_generic(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dk/dv launch");
+  }
+  return LC_OK;
+}
+
+// ---- ring descriptors ---------------------------------------------------------
+
+int check_ring(const lc_ring_desc_t* d) {
+  if (d == nullptr) return set_error(LC_ERR_INVALID, "null ring descriptor");
+  if (d->world <= 0 || d->rank < 0 || d->rank >= d->world)
+    return set_error(LC_ERR_INVALID, "rank %d out of range for world_size %d", d->rank,
+                     d->world);
+  if (d->batch <= 0 || d->heads_q <= 0 || d->heads_kv <= 0 || d->head_dim <= 0 ||
+      d->local_tokens < 0)
+    return set_error(LC_ERR_INVALID, "q, k, v must have shape [batch, tokens, heads, head_dim]");
+  if (d->heads_q % d->heads_kv != 0)
+    return set_error(LC_ERR_INVALID, "q, k, v shard shapes must match");
+  if (d->block_q <= 0 || d->block_k <= 0)
+    return set_error(LC_ERR_INVALID, "block_q and block_k must be positive");
+  if (d->local_tokens == 0) return set_error(LC_ERR_INVALID, "local_tokens must be positive");
+  if (d->valid_length >= 0 &&
+      !(0 < d->valid_length && d->valid_length <= (int64_t)d->world * d->local_tokens))
+    return set_error(LC_ERR_INVALID, "valid_length must be within the padded distributed sequence");
+  if (d->valid_length < -1) return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or positive");
+  if (d->q_position_start < -1)
+    return set_error(LC_ERR_INVALID, "q_position_start must be -1 (None) or non-negative");
+  if (d->dtype != LC_DTYPE_F32 && d->dtype != LC_DTYPE_BF16)
+    return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", d->dtype);
+  if (d->head_dim > 256)
+    return set_error(LC_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", d->head_dim);
+  return LC_OK;
+}
+
+lc::Problem ring_problem(const lc_ring_desc_t* d, int64_t q_pos0, int64_t k_pos0) {
+  lc_attn_shape_t s{d->batch, d->local_tokens, d->local_tokens, d->heads_q,
+                    d->heads_kv, d->head_dim,  d->dtype,        d->flags};
+  lc_attn_mask_t m{q_pos0, k_pos0, d->valid_length, d->causal, 0};
+  return make_problem(&s, &m);
+}
+
+struct FwdWs {
+  float* o_run;
+  float* o_part;
+  float* m_part;
+  float* l_part;
+};
+
+size_t round_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t fwd_ws_bytes(const lc_ring_desc_t* d) {
+  const size_t n_o = (size_t)d->batch * d->local_tokens * d->heads_q * d->head_dim;
+  const size_t n_s = (size_t)d->batch * d->heads_q * d->local_tokens;
+  return 2 * round_up(n_o * 4) + 2 * round_up(n_s * 4);
+}
+
+size_t bwd_ws_bytes(const lc_ring_desc_t* d) {
+  const size_t n_q = (size_t)d->batch * d->local_tokens * d->heads_q * d->head_dim;
+  const size_t n_k = (size_t)d->batch * d->local_tokens * d->heads_kv * d->head_dim;
+  const size_t n_s = (size_t)d->batch * d->heads_q * d->local_tokens;
+  return round_up(n_q * 4) + 2 * round_up(n_k * 4) + 2 * round_up(n_s * 4);
+}
+
+int check_ptrs(const void* const* arr, int world, const char* what) {
+  if (arr == nullptr) return set_error(LC_ERR_INVALID, "null %s pointer array", what);
+  for (int i = 0; i < world; ++i)
+    if (arr[i] == nullptr) return set_error(LC_ERR_INVALID, "null %s[%d]", what, i);
+  return LC_OK;
+}
+
+// Device buffer owned for the duration of a host-pointer call.
+struct DevBuf {
+  void* p = nullptr;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  hipError_t alloc(size_t bytes) { return hipMalloc(&p, bytes ? bytes : 1); }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* lc_last_error(void) { return g_last_error.c_str(); }
+
+int32_t lc_abi_version(void) { return 1; }
+
+int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                      const void* k, const void* v, float* o, float* m, float* l, void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (mask && mask->valid_length < -1)
+    return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
+  const lc::Problem p = make_problem(shape, mask);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p.Nq == 0) return LC_OK;
+  if (!pair_active(p)) {
+    hipError_t e = lc::launch_init_state(p.B, p.Nq, p.Hq, p.D, o, m, l, st);
+    return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_fwd_shard init");
+  }
+  return fwd_shard(p, q, k, v, o, m, l, st);
+}
+
+int lc_attn_merge(const lc_attn_shape_t* shape, float* o_run, float* m_run, float* l_run,
+                  const float* o_part, const float* m_part, const float* l_part, void* out,
+                  void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!o_run || !m_run || !l_run || !o_part || !m_part || !l_part)
+    return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (shape->q_tokens == 0) return LC_OK;
+  hipError_t e = lc::launch_merge(shape->batch, shape->q_tokens, shape->heads_q, shape->head_dim,
+                                  o_run, m_run, l_run, o_part, m_part, l_part, out, shape->dtype,
+                                  static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_merge launch");
+}
+
+int lc_attn_init_state(const lc_attn_shape_t* shape, float* o_run, float* m_run, float* l_run,
+                       void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!o_run || !m_run || !l_run) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (shape->q_tokens == 0) return LC_OK;
+  hipError_t e = lc::launch_init_state(shape->batch, shape->q_tokens, shape->heads_q,
+                                       shape->head_dim, o_run, m_run, l_run,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_init_state launch");
+}
+
+int lc_attn_cast(const float* src, void* dst, int64_t n, int32_t dtype, void* stream) {
+  if (dtype != LC_DTYPE_F32 && dtype != LC_DTYPE_BF16)
+    return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  if (n < 0) return set_error(LC_ERR_INVALID, "negative element count");
+  if (n == 0) return LC_OK;
+  if (!src || !dst) return set_error(LC_ERR_INVALID, "null pointer argument");
+  hipError_t e = lc::launch_cast(src, dst, n, dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_cast launch");
+}
+
+int lc_attn_bwd_preprocess(const lc_attn_shape_t* shape, const void* out, const void* dout,
+                           const float* m, const float* l, float* delta, float* lse2,
+                           void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!out || !dout || !m || !l || !delta || !lse2)
+    return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (shape->q_tokens == 0) return LC_OK;
+  hipError_t e = lc::launch_bwd_preprocess(shape->batch, shape->q_tokens, shape->heads_q,
+                                           shape->head_dim, shape->dtype, out, dout, m, l, delta,
+                                           lse2, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_bwd_preprocess launch");
+}
+
+int lc_attn_bwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                      const void* k, const void* v, const void* dout, const float* lse2,
+                      const float* delta, float* dq_acc, float* dk_acc, float* dv_acc,
+                      void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!q || !k || !v || !dout || !lse2 || !delta)
+    return set_error(LC_ERR_INVALID, "null pointer argument");
+  if ((dk_acc == nullptr) != (dv_acc == nullptr))
+    return set_error(LC_ERR_INVALID, "dk_acc and dv_acc must both be set or both be NULL");
+  if (mask && mask->valid_length < -1)
+    return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
+  const lc::Problem p = make_problem(shape, mask);
+  if (!pair_active(p)) return LC_OK;
+  return bwd_shard(p, q, k, v, dout, lse2, delta, dq_acc, dk_acc, dv_acc,
+                   static_cast<hipStream_t>(stream));
+}
+
+size_t lc_ring_fwd_workspace_bytes(const lc_ring_desc_t* desc) {
+  if (check_ring(desc) != LC_OK) return 0;
+  return fwd_ws_bytes(desc);
+}
+
+size_t lc_ring_bwd_workspace_bytes(const lc_ring_desc_t* desc) {
+  if (check_ring(desc) != LC_OK) return 0;
+  return bwd_ws_bytes(desc);
+}
+
+int lc_ring_fwd_with_stats(const lc_ring_desc_t* d, const void* const* qs, const void* const* ks,
+                           const void* const* vs, void* out, float* m, float* l, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (int rc = check_ring(d)) return rc;
+  if (int rc = check_ptrs(qs, d->world, "q")) return rc;
+  if (int rc = check_ptrs(ks, d->world, "k")) return rc;
+  if (int rc = check_ptrs(vs, d->world, "v")) return rc;
+  if (!out || !m || !l || !workspace) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (workspace_bytes < fwd_ws_bytes(d))
+    return set_error(LC_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required",
+                     workspace_bytes, fwd_ws_bytes(d));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int n = d->local_tokens;
+  const size_t n_o = (size_t)d->batch * n * d->heads_q * d->head_dim;
+  const size_t n_s = (size_t)d->batch * d->heads_q * n;
+  char* w = static_cast<char*>(workspace);
+  float* o_run = reinterpret_cast<float*>(w);
+  float* o_part = reinterpret_cast<float*>(w + round_up(n_o * 4));
+  float* m_part = reinterpret_cast<float*>(w + 2 * round_up(n_o * 4));
+  float* l_part = reinterpret_cast<float*>(w + 2 * round_up(n_o * 4) + round_up(n_s * 4));
+  const int64_t q_pos0 = d->q_position_start >= 0 ? d->q_position_start : (int64_t)d->rank * n;
+
+  // Hops with at least one unmasked pair; the others leave the reference's
+  // (m, l, acc) unchanged (alpha = 1, p = 0 in rs:36-53).
+  std::vector<int> owners;
+  for (int hop = 0; hop < d->world; ++hop) {
+    const int owner = ((d->rank - hop) % d->world + d->world) % d->world;
+    if (pair_active(ring_problem(d, q_pos0, (int64_t)owner * n))) owners.push_back(owner);
+  }
+  if (owners.empty()) {
+    LC_TRY_HIP(lc::launch_init_state(d->batch, n, d->heads_q, d->head_dim, o_run, m, l, st),
+               "lc_ring_fwd_with_stats init");
+    LC_TRY_HIP(lc::launch_cast(o_run, out, (int64_t)n_o, d->dtype, st), "lc_ring_fwd_with_stats cast");
+    return LC_OK;
+  }
+  for (size_t i = 0; i < owners.size(); ++i) {
+    const int owner = owners[i];
+    const lc::Problem p = ring_problem(d, q_pos0, (int64_t)owner * n);
+    if (i == 0) {
+      if (int rc = fwd_shard(p, qs[d->rank], ks[owner], vs[owner], o_run, m, l, st)) return rc;
+    } else {
+      if (int rc = fwd_shard(p, qs[d->rank], ks[owner], vs[owner], o_part, m_part, l_part, st))
+        return rc;
+      const bool last = (i + 1 == owners.size());
+      LC_TRY_HIP(lc::launch_merge(d->batch, n, d->heads_q, d->head_dim, o_run, m, l, o_part,
+                                  m_part, l_part, last ? out : nullptr, d->dtype, st),
+                 "lc_ring_fwd_with_stats merge");
+    }
+  }
+  if (owners.size() == 1)
+    LC_TRY_HIP(lc::launch_cast(o_run, out, (int64_t)n_o, d->dtype, st), "lc_ring_fwd_with_stats cast");
+  return LC_OK;
+}
+
+int lc_ring_bwd(const lc_ring_desc_t* d, const void* const* qs, const void* const* ks,
+                const void* const* vs, const void* const* outs, const float* const* ms,
+                const float* const* ls, const void* const* grad_outs, void* dq, void* dk,
+                void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_ring(d)) return rc;
+  if (int rc = check_ptrs(qs, d->world, "q")) return rc;
+  if (int rc = check_ptrs(ks, d->world, "k")) return rc;
+  if (int rc = check_ptrs(vs, d->world, "v")) return rc;
+  if (int rc = check_ptrs(outs, d->world, "outs")) return rc;
+  if (int rc = check_ptrs(reinterpret_cast<const void* const*>(ms), d->world, "ms")) return rc;
+  if (int rc = check_ptrs(reinterpret_cast<const void* const*>(ls), d->world, "ls")) return rc;
+  if (int rc = check_ptrs(grad_outs, d->world, "grad_outs")) return rc;
+  if (!dq || !dk || !dv || !workspace) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (workspace_bytes < bwd_ws_bytes(d))
+    return set_error(LC_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required",
+                     workspace_bytes, bwd_ws_bytes(d));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int n = d->local_tokens;
+  const int r = d->rank;
+  const size_t n_q = (size_t)d->batch * n * d->heads_q * d->head_dim;
+  const size_t n_k = (size_t)d->batch * n * d->heads_kv * d->head_dim;
+  const size_t n_s = (size_t)d->batch * d->heads_q * n;
+  char* w = static_cast<char*>(workspace);
+  float* dq_acc = reinterpret_cast<float*>(w);
+  w += round_up(n_q * 4);
+  float* dk_acc = reinterpret_cast<float*>(w);
+  w += round_up(n_k * 4);
+  float* dv_acc = reinterpret_cast<float*>(w);
+  w += round_up(n_k * 4);
+  float* delta = reinterpret_cast<float*>(w);
+  w += round_up(n_s * 4);
+  float* lse2 = reinterpret_cast<float*>(w);
+
+  LC_TRY_HIP(lc::launch_fill_zero(dq_acc, (int64_t)n_q, st), "lc_ring_bwd zero");
+  LC_TRY_HIP(lc::launch_fill_zero(dk_acc, (int64_t)n_k, st), "lc_ring_bwd zero");
+  LC_TRY_HIP(lc::launch_fill_zero(dv_acc, (int64_t)n_k, st), "lc_ring_bwd zero");
+
+  // Pass 1 (rs:367-416): local KV fixed, query owners rank, rank-1, ...;
+  // query positions owner*n + i.
+  for (int hop = 0; hop < d->world; ++hop) {
+    const int qo = ((r - hop) % d->world + d->world) % d->world;
+    const lc::Problem p = ring_problem(d, (int64_t)qo * n, (int64_t)r * n);
+    if (!pair_active(p)) continue;
+    LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[qo],
+                                         grad_outs[qo], ms[qo], ls[qo], delta, lse2, st),
+               "lc_ring_bwd preprocess");
+    if (int rc = bwd_shard(p, qs[qo], ks[r], vs[r], grad_outs[qo], lse2, delta, nullptr, dk_acc,
+                           dv_acc, st))
+      return rc;
+  }
+
+  // Pass 2 (rs:418-460): local Q fixed with positions q_position_start
+  // (default rank*n) + i, KV owners rank, rank-1, ...
+  const int64_t q_pos0 = d->q_position_start >= 0 ? d->q_position_start : (int64_t)r * n;
+  LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[r],
+                                       grad_outs[r], ms[r], ls[r], delta, lse2, st),
+             "lc_ring_bwd preprocess");
+  for (int hop = 0; hop < d->world; ++hop) {
+    const int owner = ((r - hop) % d->world + d->world) % d->world;
+    const lc::Problem p = ring_problem(d, q_pos0, (int64_t)owner * n);
+    if (!pair_active(p)) continue;
+    if (int rc = bwd_shard(p, qs[r], ks[owner], vs[owner], grad_outs[r], lse2, delta, dq_acc,
+                           nullptr, nullptr, st))
+      return rc;
+  }
+
+  LC_TRY_HIP(lc::launch_cast(dq_acc, dq, (int64_t)n_q, d->dtype, st), "lc_ring_bwd cast");
+  LC_TRY_HIP(lc::launch_cast(dk_acc, dk, (int64_t)n_k, d->dtype, st), "lc_ring_bwd cast");
+  LC_TRY_HIP(lc::launch_cast(dv_acc, dv, (int64_t)n_k, d->dtype, st), "lc_ring_bwd cast");
+  return LC_OK;
+}
+
+int lc_ring_fwd_with_stats_host(const lc_ring_desc_t* d, const void* const* qs,
+                                const void* const* ks, const void* const* vs, void* out, float* m,
+                                float* l) {
+  if (int rc = check_ring(d)) return rc;
+  if (int rc = check_ptrs(qs, d->world, "q")) return rc;
+  if (int rc = check_ptrs(ks, d->world, "k")) return rc;
+  if (int rc = check_ptrs(vs, d->world, "v")) return rc;
+  if (!out || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  const int W = d->world;
+  const size_t es = dtype_size(d->dtype);
+  const size_t q_bytes = (size_t)d->batch * d->local_tokens * d->heads_q * d->head_dim * es;
+  const size_t kv_bytes = (size_t)d->batch * d->local_tokens * d->heads_kv * d->head_dim * es;
+  const size_t s_bytes = (size_t)d->batch * d->heads_q * d->local_tokens * 4;
+  std::vector<DevBuf> kb(W), vb(W);
+  DevBuf qb, ob, mb, lb, wb;
+  std::vector<const void*> dqs(W, nullptr), dks(W), dvs(W);
+  LC_TRY_HIP(qb.alloc(q_bytes), "hipMalloc");
+  LC_TRY_HIP(hipMemcpy(qb.p, qs[d->rank], q_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  for (int i = 0; i < W; ++i) {
+    dqs[i] = qb.p;  // only this rank's queries are read
+    LC_TRY_HIP(kb[i].alloc(kv_bytes), "hipMalloc");
+    LC_TRY_HIP(vb[i].alloc(kv_bytes), "hipMalloc");
+    LC_TRY_HIP(hipMemcpy(kb[i].p, ks[i], kv_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+    LC_TRY_HIP(hipMemcpy(vb[i].p, vs[i], kv_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+    dks[i] = kb[i].p;
+    dvs[i] = vb[i].p;
+  }
+  const size_t ws = fwd_ws_bytes(d);
+  LC_TRY_HIP(ob.alloc(q_bytes), "hipMalloc");
+  LC_TRY_HIP(mb.alloc(s_bytes), "hipMalloc");
+  LC_TRY_HIP(lb.alloc(s_bytes), "hipMalloc");
+  LC_TRY_HIP(wb.alloc(ws), "hipMalloc");
+  if (int rc = lc_ring_fwd_with_stats(d, dqs.data(), dks.data(), dvs.data(), ob.p,
+                                      static_cast<float*>(mb.p), static_cast<float*>(lb.p), wb.p,
+                                      ws, nullptr))
+    return rc;
+  LC_TRY_HIP(hipDeviceSynchronize(), "lc_ring_fwd_with_stats_host");
+  LC_TRY_HIP(hipMemcpy(out, ob.p, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  LC_TRY_HIP(hipMemcpy(m, mb.p, s_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  LC_TRY_HIP(hipMemcpy(l, lb.p, s_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  return LC_OK;
+}
+
+int lc_ring_bwd_host(const lc_ring_desc_t* d, const void* const* qs, const void* const* ks,
+                     const void* const* vs, const void* const* outs, const float* const* ms,
+                     const float* const* ls, const void* const* grad_outs, void* dq, void* dk,
+                     void* dv) {
+  if (int rc = check_ring(d)) return rc;
+  if (int rc = check_ptrs(qs, d->world, "q")) return rc;
+  if (int rc = check_ptrs(ks, d->world, "k")) return rc;
+  if (int rc = check_ptrs(vs, d->world, "v")) return rc;
+  if (int rc = check_ptrs(outs, d->world, "outs")) return rc;
+  if (int rc = check_ptrs(reinterpret_cast<const void* const*>(ms), d->world, "ms")) return rc;
+  if (int rc = check_ptrs(reinterpret_cast<const void* const*>(ls), d->world, "ls")) return rc;
+  if (int rc = check_ptrs(grad_outs, d->world, "grad_outs")) return rc;
+  if (!dq || !dk || !dv) return set_error(LC_ERR_INVALID, "null pointer argument");
+  const int W = d->world;
+  const size_t es = dtype_size(d->dtype);
+  const size_t q_bytes = (size_t)d->batch * d->local_tokens * d->heads_q * d->head_dim * es;
+  const size_t kv_bytes = (size_t)d->batch * d->local_tokens * d->heads_kv * d->head_dim * es;
+  const size_t s_bytes = (size_t)d->batch * d->heads_q * d->local_tokens * 4;
+  std::vector<DevBuf> bufs(7 * W);
+  std::vector<const void*> p_q(W), p_k(W), p_v(W), p_o(W), p_g(W);
+  std::vector<const float*> p_m(W), p_l(W);
+  for (int i = 0; i < W; ++i) {
+    const void* src[7] = {qs[i], ks[i], vs[i], outs[i], grad_outs[i], ms[i], ls[i]};
+    const size_t sz[7] = {q_bytes, kv_bytes, kv_bytes, q_bytes, q_bytes, s_bytes, s_bytes};
+    for (int j = 0; j < 7; ++j) {
+      DevBuf& b = bufs[7 * i + j];
+      LC_TRY_HIP(b.alloc(sz[j]), "hipMalloc");
+      LC_TRY_HIP(hipMemcpy(b.p, src[j], sz[j], hipMemcpyHostToDevice), "hipMemcpy");
+    }
+    p_q[i] = bufs[7 * i].p;
+    p_k[i] = bufs[7 * i + 1].p;
+    p_v[i] = bufs[7 * i + 2].p;
+    p_o[i] = bufs[7 * i + 3].p;
+    p_g[i] = bufs[7 * i + 4].p;
+    p_m[i] = static_cast<const float*>(bufs[7 * i + 5].p);
+    p_l[i] = static_cast<const float*>(bufs[7 * i + 6].p);
+  }
+  DevBuf dqb, dkb, dvb, wb;
+  const size_t ws = bwd_ws_bytes(d);
+  LC_TRY_HIP(dqb.alloc(q_bytes), "hipMalloc");
+  LC_TRY_HIP(dkb.alloc(kv_bytes), "hipMalloc");
+  LC_TRY_HIP(dvb.alloc(kv_bytes), "hipMalloc");
+  LC_TRY_HIP(wb.alloc(ws), "hipMalloc");
+  if (int rc = lc_ring_bwd(d, p_q.data(), p_k.data(), p_v.data(), p_o.data(), p_m.data(),
+                           p_l.data(), p_g.data(), dqb.p, dkb.p, dvb.p, wb.p, ws, nullptr))
+    return rc;
+  LC_TRY_HIP(hipDeviceSynchronize(), "lc_ring_bwd_host");
+  LC_TRY_HIP(hipMemcpy(dq, dqb.p, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  LC_TRY_HIP(hipMemcpy(dk, dkb.p, kv_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  LC_TRY_HIP(hipMemcpy(dv, dvb.p, kv_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  return LC_OK;
+}
+
+int lc_reference_causal_attention_host(int32_t batch, int32_t tokens, int32_t heads_q,
+                                       int32_t heads_kv, int32_t head_dim, int32_t dtype,
+                                       const void* q, const void* k, const void* v, int32_t causal,
+                                       int64_t valid_length, void* out) {
+  lc_ring_desc_t d{};
+  d.world = 1;
+  d.rank = 0;
+  d.batch = batch;
+  d.local_tokens = tokens;
+  d.heads_q = heads_q;
+  d.heads_kv = heads_kv;
+  d.head_dim = head_dim;
+  d.dtype = dtype;
+  d.flags = 0;
+  d.causal = causal;
+  d.block_q = 64;
+  d.block_k = 128;
+  d.valid_length = valid_length;
+  d.q_position_start = -1;
+  if (!q || !k || !v || !out) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (int rc = check_ring(&d)) return rc;
+  const void* qs[1] = {q};
+  const void* ks[1] = {k};
+  const void* vs[1] = {v};
+  std::vector<float> m((size_t)batch * heads_q * tokens), l(m.size());
+  return lc_ring_fwd_with_stats_host(&d, qs, ks, vs, out, m.data(), l.data());
+}
+
+}  // extern "C"

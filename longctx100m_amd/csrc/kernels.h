@@ -1,0 +1,66 @@
+// Internal launcher interface between the C-ABI host code (api.cpp) and the
+// HIP kernel translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lc {
+
+// One (query shard x KV shard) problem after validation.
+struct Problem {
+  int B, Nq, Nk, Hq, Hkv, D;
+  int dtype;  // 0 = f32, 1 = bf16
+  bool precise;
+  int64_t q_pos0, k_pos0;
+  int64_t valid;  // INT64_MAX when the reference's valid_length is None
+  bool causal;
+  float scale;  // D^-1/2
+};
+
+// Index of the exclusive end of the keys that any query of [q_begin, q_end)
+// can see, clipped to [0, Nk].
+inline int64_t key_end_for(const Problem& p, int64_t q_end) {
+  int64_t kend = p.Nk;
+  if (p.causal) {
+    const int64_t last_q = p.q_pos0 + q_end - 1;
+    if (last_q - p.k_pos0 + 1 < kend) kend = last_q - p.k_pos0 + 1;
+  }
+  if (p.valid - p.k_pos0 < kend) kend = p.valid - p.k_pos0;
+  return kend < 0 ? 0 : kend;
+}
+
+// True when the bf16 MFMA kernels implement this problem.
+bool mfma_supported(const Problem& p);
+
+hipError_t launch_fwd_mfma(const Problem& p, const void* q, const void* k, const void* v, float* o,
+                           float* m, float* l, hipStream_t s);
+hipError_t launch_fwd_generic(const Problem& p, const void* q, const void* k, const void* v,
+                              float* o, float* m, float* l, hipStream_t s);
+
+hipError_t launch_bwd_dq_mfma(const Problem& p, const void* q, const void* k, const void* v,
+                              const void* dout, const float* lse2, const float* delta, float* dq,
+                              hipStream_t s);
+hipError_t launch_bwd_dkdv_mfma(const Problem& p, const void* q, const void* k, const void* v,
+                                const void* dout, const float* lse2, const float* delta, float* dk,
+                                float* dv, hipStream_t s);
+hipError_t launch_bwd_dq_generic(const Problem& p, const void* q, const void* k, const void* v,
+                                 const void* dout, const float* lse2, const float* delta,
+                                 float* dq, hipStream_t s);
+hipError_t launch_bwd_dkdv_generic(const Problem& p, const void* q, const void* k, const void* v,
+                                   const void* dout, const float* lse2, const float* delta,
+                                   float* dk, float* dv, hipStream_t s);
+
+// Row-wise helpers.  rows = B * N * H, row r = ((b * N) + t) * H + h.
+hipError_t launch_merge(int B, int N, int H, int D, float* o_run, float* m_run, float* l_run,
+                        const float* o_part, const float* m_part, const float* l_part, void* out,
+                        int out_dtype, hipStream_t s);
+hipError_t launch_init_state(int B, int N, int H, int D, float* o, float* m, float* l,
+                             hipStream_t s);
+hipError_t launch_cast(const float* src, void* dst, int64_t n, int dtype, hipStream_t s);
+hipError_t launch_fill_zero(float* dst, int64_t n, hipStream_t s);
+hipError_t launch_bwd_preprocess(int B, int N, int H, int D, int dtype, const void* out,
+                                 const void* dout, const float* m, const float* l, float* delta,
+                                 float* lse2, hipStream_t s);
+
+}  // namespace lc

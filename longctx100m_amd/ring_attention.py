@@ -1,0 +1,270 @@
+"""Torch-facing mirror of the reference's ring-attention API, on MI355X.
+
+Function names, argument meaning and error behaviour follow the reference's
+Rust module (rust/longctx100m-model/src/ring_attention.rs, re-exported at
+lib.rs:16-19):
+
+* ring_causal_attention_forward            rs:116-135
+* ring_causal_attention_forward_with_stats rs:139-233
+* ring_causal_attention_backward           rs:281-475
+* reference_causal_attention               rs:237-270
+
+``shards`` is every rank's (q, k, v) triple in rank order, each a contiguous
+``[B, local_tokens, H, D]`` tensor on the GPU; the ring is emulated on one GPU
+as an ordered loop over the KV shards held in HBM.  Unlike the reference,
+K/V may carry fewer heads than Q (GQA, query head h reads KV head
+h // (Hq // Hkv)); the reference's callers expand with repeat_interleave
+instead (model.rs:85-94).
+
+The per-hop building blocks (``fwd_shard``, ``merge``, ``bwd_preprocess``,
+``bwd_shard``) expose the C ABI one kernel step at a time, the shape a real
+xGMI ring drives them in.  Everything runs through liblongctx100m_attn.so;
+there is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.LC_DTYPE_F32, torch.bfloat16: _lib.LC_DTYPE_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _check_dev(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError("expected torch tensors")
+        if not t.is_cuda:
+            raise ValueError("tensors must live on the GPU (device pointers are passed to HIP)")
+        if not t.is_contiguous():
+            raise ValueError("tensors must be contiguous")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _opt(x: Optional[int]) -> int:
+    return -1 if x is None else int(x)
+
+
+def _shape(q: torch.Tensor, k: torch.Tensor, precise: bool) -> _lib.Shape:
+    if q.ndim != 4 or k.ndim != 4:
+        raise ValueError("q, k, v must have shape [batch, tokens, heads, head_dim]")
+    b, nq, hq, d = q.shape
+    bk, nk, hkv, dk = k.shape
+    if b != bk or d != dk:
+        raise ValueError("q, k, v shard shapes must match")
+    flags = _lib.LC_FLAG_PRECISE if precise else 0
+    return _lib.Shape(b, nq, nk, hq, hkv, d, _dtype_code(q), flags)
+
+
+# ---------------------------------------------------------------- per hop ----
+
+def fwd_shard(q, k, v, *, q_pos0: int, k_pos0: int, causal: bool = True,
+              valid_length: Optional[int] = None, precise: bool = False,
+              o: Optional[torch.Tensor] = None, m: Optional[torch.Tensor] = None,
+              l: Optional[torch.Tensor] = None):
+    """One hop: attention of the query shard over one KV shard.
+
+    Returns (o [B,Nq,Hq,D] fp32 normalised, m [B,Hq,Nq], l [B,Hq,Nq])."""
+    _check_dev(q, k, v)
+    if k.shape != v.shape or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v shard shapes must match")
+    s = _shape(q, k, precise)
+    b, nq, hq, d = q.shape
+    o = torch.empty((b, nq, hq, d), dtype=torch.float32, device=q.device) if o is None else o
+    m = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if m is None else m
+    l = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if l is None else l
+    mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
+    _lib.check(_lib.load().lc_attn_fwd_shard(s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             o.data_ptr(), m.data_ptr(), l.data_ptr(), _stream()))
+    return o, m, l
+
+
+def merge(o_run, m_run, l_run, o_part, m_part, l_part, out: Optional[torch.Tensor] = None):
+    """In-place LSE merge of a hop's partial into the running state; optionally
+    also writes the merged output cast to ``out``'s dtype."""
+    _check_dev(o_run, m_run, l_run, o_part, m_part, l_part)
+    b, nq, hq, d = o_run.shape
+    dt = _lib.LC_DTYPE_F32 if out is None else _dtype_code(out)
+    s = _lib.Shape(b, nq, nq, hq, hq, d, dt, 0)
+    _lib.check(_lib.load().lc_attn_merge(s, o_run.data_ptr(), m_run.data_ptr(), l_run.data_ptr(),
+                                         o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(),
+                                         None if out is None else out.data_ptr(), _stream()))
+
+
+def cast(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    _check_dev(src, dst)
+    if src.dtype != torch.float32 or src.numel() != dst.numel():
+        raise ValueError("cast takes an fp32 source of the destination's size")
+    _lib.check(_lib.load().lc_attn_cast(src.data_ptr(), dst.data_ptr(), src.numel(),
+                                        _dtype_code(dst), _stream()))
+    return dst
+
+
+def bwd_preprocess(out, dout, m, l, delta=None, lse2=None):
+    """delta = rowsum(dout * out), lse2 = m*log2(e) + log2(max(l, FLT_MIN))."""
+    _check_dev(out, dout, m, l)
+    b, nq, hq, d = out.shape
+    delta = torch.empty((b, hq, nq), dtype=torch.float32, device=out.device) if delta is None else delta
+    lse2 = torch.empty_like(delta) if lse2 is None else lse2
+    s = _lib.Shape(b, nq, nq, hq, hq, d, _dtype_code(out), 0)
+    _lib.check(_lib.load().lc_attn_bwd_preprocess(s, out.data_ptr(), dout.data_ptr(),
+                                                  m.data_ptr(), l.data_ptr(), delta.data_ptr(),
+                                                  lse2.data_ptr(), _stream()))
+    return delta, lse2
+
+
+def bwd_shard(q, k, v, dout, lse2, delta, *, q_pos0: int, k_pos0: int, causal: bool = True,
+              valid_length: Optional[int] = None, dq_acc=None, dk_acc=None, dv_acc=None,
+              precise: bool = False):
+    """One hop of the backward; adds into the fp32 accumulators given."""
+    _check_dev(q, k, v, dout, lse2, delta)
+    s = _shape(q, k, precise)
+    mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    _lib.check(_lib.load().lc_attn_bwd_shard(s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             dout.data_ptr(), lse2.data_ptr(), delta.data_ptr(),
+                                             ptr(dq_acc), ptr(dk_acc), ptr(dv_acc), _stream()))
+
+
+# ------------------------------------------------------- reference signatures --
+
+def _ring_desc(shards, rank, causal, block_q, block_k, valid_length, q_position_start, precise):
+    world = len(shards)
+    if world == 0:
+        raise ValueError(f"rank {rank} out of range for world_size {world}")
+    q, k, v = shards[0]
+    for (qq, kk, vv) in shards:
+        _check_dev(qq, kk, vv)
+        if qq.ndim != 4 or kk.ndim != 4 or vv.ndim != 4:
+            raise ValueError("q, k, v must have shape [batch, tokens, heads, head_dim]")
+        if (qq.shape != q.shape or kk.shape != k.shape or vv.shape != k.shape
+                or qq.dtype != q.dtype or kk.dtype != q.dtype or vv.dtype != q.dtype):
+            raise ValueError("q, k, v shard shapes must match")
+    b, n, hq, d = q.shape
+    if k.shape[0] != b or k.shape[1] != n or k.shape[3] != d:
+        raise ValueError("q, k, v shard shapes must match")
+    flags = _lib.LC_FLAG_PRECISE if precise else 0
+    return _lib.RingDesc(world, rank, b, n, hq, k.shape[2], d, _dtype_code(q), flags,
+                         int(causal), block_q, block_k, _opt(valid_length),
+                         _opt(q_position_start))
+
+
+def ring_causal_attention_forward_with_stats(
+        shards: Sequence[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]], rank: int,
+        causal: bool = True, block_q: int = 64, block_k: int = 128,
+        valid_length: Optional[int] = None, q_position_start: Optional[int] = None,
+        *, precise: bool = False):
+    """(out [B,n,Hq,D] in the input dtype, m [B,Hq,n,1] fp32, l [B,Hq,n,1] fp32)."""
+    desc = _ring_desc(shards, rank, causal, block_q, block_k, valid_length, q_position_start,
+                      precise)
+    if not 0 <= rank < len(shards):
+        raise ValueError(f"rank {rank} out of range for world_size {len(shards)}")
+    lib = _lib.load()
+    q = shards[rank][0]
+    b, n, hq, d = q.shape
+    out = torch.empty_like(q)
+    m = torch.empty((b, hq, n, 1), dtype=torch.float32, device=q.device)
+    l = torch.empty_like(m)
+    ws_bytes = lib.lc_ring_fwd_workspace_bytes(desc)
+    if ws_bytes == 0:
+        _lib.check(lib.lc_ring_fwd_with_stats(desc, None, None, None, None, None, None, None, 0,
+                                              None))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    qs, _a = _lib.ptr_array([s[0].data_ptr() for s in shards])
+    ks, _b = _lib.ptr_array([s[1].data_ptr() for s in shards])
+    vs, _c = _lib.ptr_array([s[2].data_ptr() for s in shards])
+    _lib.check(lib.lc_ring_fwd_with_stats(desc, qs, ks, vs, out.data_ptr(), m.data_ptr(),
+                                          l.data_ptr(), ws.data_ptr(), ws_bytes, _stream()))
+    return out, m, l
+
+
+def ring_causal_attention_forward(shards, rank, causal=True, block_q=64, block_k=128,
+                                  valid_length=None, q_position_start=None, *, precise=False):
+    out, _, _ = ring_causal_attention_forward_with_stats(
+        shards, rank, causal, block_q, block_k, valid_length, q_position_start, precise=precise)
+    return out
+
+
+def ring_causal_attention_backward(shards, rank, outs, ms, ls, grad_outs, causal=True,
+                                   block_q=64, block_k=128, valid_length=None,
+                                   q_position_start=None, *, precise=False):
+    """(dq [B,n,Hq,D], dk [B,n,Hkv,D], dv [B,n,Hkv,D]) of rank ``rank``'s shard."""
+    desc = _ring_desc(shards, rank, causal, block_q, block_k, valid_length, q_position_start,
+                      precise)
+    world = len(shards)
+    if not 0 <= rank < world:
+        raise ValueError(f"rank {rank} out of range for world_size {world}")
+    if not (len(outs) == len(ms) == len(ls) == len(grad_outs) == world):
+        raise ValueError("outs, ms, ls and grad_outs must hold one tensor per rank")
+    q, k, _ = shards[rank]
+    for t in (*outs, *grad_outs):
+        _check_dev(t)
+        if t.shape != q.shape or t.dtype != q.dtype:
+            raise ValueError("outs and grad_outs must match the query shard")
+    ms = [x.float().contiguous() for x in ms]
+    ls = [x.float().contiguous() for x in ls]
+    lib = _lib.load()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(k)
+    ws_bytes = lib.lc_ring_bwd_workspace_bytes(desc)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    arrs = [_lib.ptr_array([t.data_ptr() for t in ts]) for ts in
+            ([s[0] for s in shards], [s[1] for s in shards], [s[2] for s in shards], outs, ms,
+             ls, grad_outs)]
+    _lib.check(lib.lc_ring_bwd(desc, *[a[0] for a in arrs], dq.data_ptr(), dk.data_ptr(),
+                               dv.data_ptr(), ws.data_ptr(), ws_bytes, _stream()))
+    return dq, dk, dv
+
+
+def reference_causal_attention(q, k, v, causal: bool = True,
+                               valid_length: Optional[int] = None, *, precise: bool = False):
+    """Dense attention of one [B,T,H,D] sequence (a one-rank ring)."""
+    return ring_causal_attention_forward([(q, k, v)], 0, causal, 64, 128, valid_length, None,
+                                         precise=precise)
+
+
+class RingCausalAttention(torch.autograd.Function):
+    """Autograd wrapper of one rank's share, mirroring _RingCausalAttention
+    (src/longctx100m/ring_attention.py:194-255) with the in-process ring: the
+    forward saves (out, m, l) and the backward recomputes P from them.
+
+    Gradients flow to this rank's q, k and v; the other ranks' shards are
+    treated as constants (their owners differentiate their own shares)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, shards, rank, causal, valid_length):
+        shards = list(shards)
+        shards[rank] = (q.detach(), k.detach(), v.detach())
+        outs, ms, ls = [], [], []
+        for r in range(len(shards)):
+            o, m, l = ring_causal_attention_forward_with_stats(shards, r, causal, 64, 128,
+                                                               valid_length)
+            outs.append(o)
+            ms.append(m)
+            ls.append(l)
+        ctx.shards, ctx.rank, ctx.causal, ctx.valid_length = shards, rank, causal, valid_length
+        ctx.outs, ctx.ms, ctx.ls = outs, ms, ls
+        return outs[rank]
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        grad_outs = [torch.zeros_like(o) for o in ctx.outs]
+        grad_outs[ctx.rank] = grad_out.contiguous()
+        dq, dk, dv = ring_causal_attention_backward(ctx.shards, ctx.rank, ctx.outs, ctx.ms,
+                                                    ctx.ls, grad_outs, ctx.causal, 64, 128,
+                                                    ctx.valid_length)
+        return dq, dk, dv, None, None, None, None

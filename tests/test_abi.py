@@ -1,0 +1,127 @@
+"""The C-ABI library loads, exports exactly what include/longctx100m_attn.h
+declares, and rejects bad arguments with the reference's messages
+(rust/longctx100m-model/src/ring_attention.rs:148-171) before touching the
+GPU.  Runs without a GPU: no compute entry point is reached."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from longctx100m_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "longctx100m_attn.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lc_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    declared = header_functions()
+    assert len(declared) >= 15
+    assert sorted(_lib.SIGNATURES) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.lc_abi_version() == 1
+
+
+def test_struct_layouts_match_header():
+    assert ctypes.sizeof(_lib.Shape) == 32
+    assert ctypes.sizeof(_lib.Mask) == 32
+    assert ctypes.sizeof(_lib.RingDesc) == 64
+    assert _lib.RingDesc.valid_length.offset == 48
+
+
+def _desc(**kw):
+    d = dict(world=2, rank=0, batch=1, local_tokens=8, heads_q=4, heads_kv=2, head_dim=64,
+             dtype=_lib.LC_DTYPE_BF16, flags=0, causal=1, block_q=64, block_k=128,
+             valid_length=-1, q_position_start=-1)
+    d.update(kw)
+    return _lib.RingDesc(**d)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(rank=2), _lib.LC_ERR_INVALID, "rank 2 out of range for world_size 2"),
+    (dict(block_q=0), _lib.LC_ERR_INVALID, "block_q and block_k must be positive"),
+    (dict(block_k=-3), _lib.LC_ERR_INVALID, "block_q and block_k must be positive"),
+    (dict(local_tokens=0), _lib.LC_ERR_INVALID, "local_tokens must be positive"),
+    (dict(valid_length=17), _lib.LC_ERR_INVALID,
+     "valid_length must be within the padded distributed sequence"),
+    (dict(valid_length=0), _lib.LC_ERR_INVALID,
+     "valid_length must be within the padded distributed sequence"),
+    (dict(heads_kv=3), _lib.LC_ERR_INVALID, "q, k, v shard shapes must match"),
+    (dict(head_dim=0), _lib.LC_ERR_INVALID,
+     "q, k, v must have shape [batch, tokens, heads, head_dim]"),
+    (dict(dtype=7), _lib.LC_ERR_UNSUPPORTED, "unsupported dtype 7"),
+])
+def test_ring_validation_messages(lib, kw, code, msg):
+    d = _desc(**kw)
+    assert lib.lc_ring_fwd_workspace_bytes(d) == 0
+    rc = lib.lc_ring_fwd_with_stats(d, None, None, None, None, None, None, None, 0, None)
+    assert rc == code
+    assert lib.lc_last_error().decode() == msg
+    rc = lib.lc_ring_bwd(d, None, None, None, None, None, None, None, None, None, None, None, 0,
+                         None)
+    assert rc == code
+    assert lib.lc_last_error().decode() == msg
+    with pytest.raises(ValueError if code == _lib.LC_ERR_INVALID else _lib.LcError, match=re.escape(msg)):
+        _lib.check(rc)
+
+
+def test_workspace_sizes(lib):
+    d = _desc(local_tokens=32768, heads_q=16, heads_kv=16, head_dim=128, world=8, rank=7)
+    n_o = 32768 * 16 * 128
+    n_s = 16 * 32768
+    assert lib.lc_ring_fwd_workspace_bytes(d) == 2 * 4 * n_o + 2 * 4 * n_s
+    assert lib.lc_ring_bwd_workspace_bytes(d) == 3 * 4 * n_o + 2 * 4 * n_s
+
+
+def test_null_and_workspace_errors(lib):
+    d = _desc()
+    ptrs = (ctypes.c_void_p * 2)(1, 2)
+    pp = ctypes.cast(ptrs, ctypes.POINTER(ctypes.c_void_p))
+    rc = lib.lc_ring_fwd_with_stats(d, pp, pp, pp, 16, 16, 16, 16, 1, None)
+    assert rc == _lib.LC_ERR_WORKSPACE
+    assert "workspace" in lib.lc_last_error().decode()
+    rc = lib.lc_ring_fwd_with_stats(d, None, pp, pp, 16, 16, 16, 16, 1 << 30, None)
+    assert rc == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == "null q pointer array"
+    shape = _lib.Shape(1, 4, 4, 2, 2, 64, _lib.LC_DTYPE_BF16, 0)
+    rc = lib.lc_attn_fwd_shard(shape, None, None, None, None, None, None, None, None)
+    assert rc == _lib.LC_ERR_INVALID
+    bad = _lib.Shape(1, 4, 4, 3, 2, 64, _lib.LC_DTYPE_BF16, 0)
+    rc = lib.lc_attn_fwd_shard(bad, None, 16, 16, 16, 16, 16, 16, None)
+    assert rc == _lib.LC_ERR_INVALID
+    assert "multiple of heads_kv" in lib.lc_last_error().decode()
+    big = _lib.Shape(1, 4, 4, 2, 2, 512, _lib.LC_DTYPE_F32, 0)
+    rc = lib.lc_attn_fwd_shard(big, None, 16, 16, 16, 16, 16, 16, None)
+    assert rc == _lib.LC_ERR_UNSUPPORTED
+    rc = lib.lc_attn_cast(None, None, 10, 5, None)
+    assert rc == _lib.LC_ERR_UNSUPPORTED
+
+
+def test_last_error_is_per_thread(lib):
+    import threading
+
+    lib.lc_ring_fwd_with_stats(_desc(rank=5), None, None, None, None, None, None, None, 0, None)
+    seen = {}
+
+    def other():
+        lib.lc_ring_fwd_with_stats(_desc(block_q=0), None, None, None, None, None, None, None, 0,
+                                   None)
+        seen["msg"] = lib.lc_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == "block_q and block_k must be positive"
+    assert lib.lc_last_error().decode() == "rank 5 out of range for world_size 2"

@@ -1,0 +1,350 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the oracle.
+
+Bars (BASELINE config notes): fp32 path within 1e-5 and bf16 path within
+2e-2, both norm-relative (max|a-b| / max|b|).  bf16 references are computed
+in fp32/fp64 on the bf16-rounded inputs, with the forward output rounded to
+bf16 before it enters delta, the reference's bf16 rule
+(src/longctx100m/ring_attention.py:17,28,151,314).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import dense, ring
+from tests.conftest import norm_rel
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+FP32_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def ra(gpu):
+    from longctx100m_amd import ring_attention
+
+    return ring_attention
+
+
+def _t(gpu, arr, dtype):
+    return gpu.tensor(np.ascontiguousarray(arr), dtype=gpu.float32).to(dtype).cuda()
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rand_shards(gpu, rng, world, n, hq, hkv, d, dtype, b=1):
+    qs, ks, vs = [], [], []
+    for _ in range(world):
+        qs.append(_t(gpu, rng.standard_normal((b, n, hq, d)), dtype))
+        ks.append(_t(gpu, rng.standard_normal((b, n, hkv, d)), dtype))
+        vs.append(_t(gpu, rng.standard_normal((b, n, hkv, d)), dtype))
+    return qs, ks, vs
+
+
+# ------------------------------------------------------------- per-hop kernels --
+
+FWD_CASES = [
+    # nq, nk, hq, hkv, d, q_pos0, k_pos0, causal, valid
+    (256, 256, 2, 2, 128, 0, 0, True, None),      # diagonal block
+    (300, 200, 4, 2, 128, 500, 100, True, None),  # tails, GQA, offsets
+    (200, 333, 2, 1, 64, 100, 0, True, 250),      # d=64, valid_length
+    (128, 192, 2, 2, 128, 0, 0, False, None),     # non-causal
+    (96, 64, 3, 1, 128, 0, 64, True, None),       # partly fully-masked rows
+    (64, 64, 1, 1, 128, 0, 64, True, None),       # keys after every query
+]
+
+
+@pytest.mark.parametrize("precise", [False, True])
+@pytest.mark.parametrize("case", FWD_CASES)
+def test_fwd_shard_bf16(ra, gpu, case, precise):
+    nq, nk, hq, hkv, d, qp, kp, causal, valid = case
+    rng = np.random.default_rng(hash(case) % 2**32)
+    q = _t(gpu, rng.standard_normal((1, nq, hq, d)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.bfloat16)
+    o, m, l = ra.fwd_shard(q, k, v, q_pos0=qp, k_pos0=kp, causal=causal, valid_length=valid,
+                           precise=precise)
+    gpu.cuda.synchronize()
+    eo, em, el = dense.attention_fwd(_np(q), _np(k), _np(v), causal=causal, valid_length=valid,
+                                     q_pos0=qp, k_pos0=kp)
+    tol = FP32_TOL if precise else BF16_TOL
+    assert norm_rel(_np(o), eo) <= tol
+    m, l = _np(m), _np(l)
+    fin = np.isfinite(em)
+    assert np.array_equal(np.isfinite(m), fin)
+    if fin.any():
+        assert np.abs(m[fin] - em[fin]).max() <= 1e-4 * max(1.0, np.abs(em[fin]).max())
+        assert norm_rel(l, el) <= 1e-4
+    assert np.all(l[~fin] == 0) and np.all(_np(o)[:, ~fin[0].T] == 0)
+
+
+@pytest.mark.parametrize("case", FWD_CASES[:4])
+def test_fwd_shard_fp32(ra, gpu, case):
+    nq, nk, hq, hkv, d, qp, kp, causal, valid = case
+    rng = np.random.default_rng(7 + nq)
+    q = _t(gpu, rng.standard_normal((1, nq, hq, d)), gpu.float32)
+    k = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.float32)
+    v = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.float32)
+    o, m, l = ra.fwd_shard(q, k, v, q_pos0=qp, k_pos0=kp, causal=causal, valid_length=valid)
+    gpu.cuda.synchronize()
+    eo, em, el = dense.attention_fwd(_np(q), _np(k), _np(v), causal=causal, valid_length=valid,
+                                     q_pos0=qp, k_pos0=kp)
+    assert norm_rel(_np(o), eo) <= FP32_TOL
+    assert np.abs(_np(m) - em).max() <= 1e-5 * max(1.0, np.abs(em).max())
+    assert norm_rel(_np(l), el) <= FP32_TOL
+
+
+BWD_CASES = [
+    (256, 256, 2, 2, 128, 0, 0, True, None),
+    (300, 200, 4, 2, 128, 500, 100, True, None),
+    (200, 333, 2, 1, 64, 100, 0, True, 250),
+    (160, 130, 4, 1, 128, 0, 0, False, None),
+]
+
+
+@pytest.mark.parametrize("dtype_name,precise", [("bfloat16", False), ("bfloat16", True),
+                                                ("float32", False)])
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_bwd_shard(ra, gpu, case, dtype_name, precise):
+    nq, nk, hq, hkv, d, qp, kp, causal, valid = case
+    dtype = getattr(gpu, dtype_name)
+    rng = np.random.default_rng(31 + nq + nk)
+    q = _t(gpu, rng.standard_normal((1, nq, hq, d)), dtype)
+    k = _t(gpu, rng.standard_normal((1, nk, hkv, d)), dtype)
+    v = _t(gpu, rng.standard_normal((1, nk, hkv, d)), dtype)
+    do = _t(gpu, rng.standard_normal((1, nq, hq, d)), dtype)
+    kw = dict(q_pos0=qp, k_pos0=kp, causal=causal, valid_length=valid)
+    o32, m, l = ra.fwd_shard(q, k, v, precise=precise, **kw)
+    out = o32.to(dtype)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    dq = gpu.zeros((1, nq, hq, d), dtype=gpu.float32, device="cuda")
+    dk = gpu.zeros((1, nk, hkv, d), dtype=gpu.float32, device="cuda")
+    dv = gpu.zeros_like(dk)
+    ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, precise=precise, **kw)
+    gpu.cuda.synchronize()
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **kw)
+    tol = FP32_TOL if (dtype_name == "float32" or precise) else BF16_TOL
+    if dtype_name == "float32":
+        tol = 2e-5  # fp32 reductions over ~300 terms; the reference's own bar is 1e-4 abs
+    assert norm_rel(_np(dq), edq) <= tol
+    assert norm_rel(_np(dk), edk) <= tol
+    assert norm_rel(_np(dv), edv) <= tol
+
+
+def test_merge_is_order_invariant(ra, gpu):
+    rng = np.random.default_rng(5)
+    nq, hq, d = 192, 2, 128
+    q = _t(gpu, rng.standard_normal((1, nq, hq, d)), gpu.bfloat16)
+    kv = [(_t(gpu, rng.standard_normal((1, 100, hq, d)), gpu.bfloat16),
+           _t(gpu, rng.standard_normal((1, 100, hq, d)), gpu.bfloat16)) for _ in range(3)]
+    parts = [ra.fwd_shard(q, k, v, q_pos0=300, k_pos0=100 * i) for i, (k, v) in enumerate(kv)]
+    results = []
+    for order in ([0, 1, 2], [2, 0, 1], [1, 2, 0]):
+        o, m, l = (x.clone() for x in parts[order[0]])
+        for j in order[1:]:
+            ra.merge(o, m, l, *parts[j])
+        results.append((_np(o), _np(m), _np(l)))
+    k_all = np.concatenate([_np(k) for k, _ in kv], axis=1)
+    v_all = np.concatenate([_np(v) for _, v in kv], axis=1)
+    eo, em, el = dense.attention_fwd(_np(q), k_all, v_all, q_pos0=300, k_pos0=0)
+    for o, m, l in results:
+        assert norm_rel(o, eo) <= BF16_TOL
+        assert np.abs(m - em).max() <= 1e-4 * np.abs(em).max()
+        assert norm_rel(l, el) <= 1e-4
+    for o, m, l in results[1:]:
+        assert norm_rel(o, results[0][0]) <= 1e-5
+
+
+# ------------------------------------------------------------------ whole ring --
+
+def _oracle_ring(qs, ks, vs, world, hq, hkv, rank=None, gos=None, **kw):
+    """C-restatement results on the (rounded) inputs, KV heads expanded by
+    repeat_interleave as the reference's callers do; returns per-rank
+    (out, m, l) and, if gos is given, rank's (dq, dk, dv) with dk/dv summed
+    over each GQA group."""
+    g = hq // hkv
+    qn = [_np(x) for x in qs]
+    kn = [np.repeat(_np(x), g, axis=2) for x in ks]
+    vn = [np.repeat(_np(x), g, axis=2) for x in vs]
+    fw = [ring.ring_fwd_with_stats(qn, kn, vn, r, **kw) for r in range(world)]
+    if gos is None:
+        return fw, None
+    dtype_round = qs[0].dtype
+    import torch
+
+    outs = [torch.tensor(o).to(dtype_round).float().numpy() for o, _, _ in fw]
+    dq, dk, dv = ring.ring_bwd(qn, kn, vn, outs, [x[1] for x in fw], [x[2] for x in fw],
+                               [_np(x) for x in gos], rank, **kw)
+    b, n, _, d = dk.shape
+    return fw, (dq, dk.reshape(b, n, hkv, g, d).sum(3), dv.reshape(b, n, hkv, g, d).sum(3))
+
+
+@pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
+def test_ring_config1(ra, gpu, dtype_name):
+    """world 2 x 512 tokens, Hq=9, Hkv=3 (GQA), d=64."""
+    dtype = getattr(gpu, dtype_name)
+    tol = FP32_TOL if dtype_name == "float32" else BF16_TOL
+    rng = np.random.default_rng(1)
+    world, n, hq, hkv, d = 2, 512, 9, 3, 64
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, hq, hkv, d, dtype)
+    gos = [_t(gpu, rng.standard_normal((1, n, hq, d)), dtype) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    outs, ms, ls = [], [], []
+    for r in range(world):
+        o, m, l = ra.ring_causal_attention_forward_with_stats(shards, r)
+        outs.append(o)
+        ms.append(m)
+        ls.append(l)
+    gpu.cuda.synchronize()
+    for r in range(world):
+        fw, grads = _oracle_ring(qs, ks, vs, world, hq, hkv, rank=r, gos=gos)
+        eo, em, el = fw[r]
+        assert norm_rel(_np(outs[r]), eo) <= tol
+        assert np.abs(_np(ms[r])[..., 0] - em).max() <= 1e-4 * np.abs(em).max()
+        assert norm_rel(_np(ls[r])[..., 0], el) <= 1e-4
+        dq, dk, dv = ra.ring_causal_attention_backward(shards, r, outs, ms, ls, gos)
+        gpu.cuda.synchronize()
+        for a, b in zip((dq, dk, dv), grads):
+            assert norm_rel(_np(a), b) <= tol
+
+
+def test_reference_unit_cases_on_gpu(ra, gpu):
+    """The reference's Rust unit tests (ring_attention.rs:519-668) through
+    the HIP path, fp32, same shapes, blocks and tolerances."""
+    f32 = gpu.float32
+    rng = np.random.default_rng(0)
+    q, k, v = (_t(gpu, rng.standard_normal((1, 8, 2, 4)), f32) for _ in range(3))
+    out = ra.ring_causal_attention_forward([(q, k, v)], 0, True, 2, 3, None, None)
+    exp = dense.attention_fwd(_np(q), _np(k), _np(v))[0]
+    assert np.abs(_np(out) - exp).max() < 1e-5
+    ref = ra.reference_causal_attention(q, k, v)
+    assert np.abs(_np(ref) - exp).max() < 1e-5
+    for valid in (None, 6):
+        qs = [_t(gpu, x, f32) for x in dense.lcg_shards(4, 2, 4, 2)]
+        shards = [(x, x, x) for x in qs]
+        full = np.concatenate([_np(x) for x in qs], axis=1)
+        e = dense.attention_fwd(full, full, full, valid_length=valid)[0]
+        for r in range(2):
+            o = ra.ring_causal_attention_forward(shards, r, True, 2, 3, valid, None)
+            assert np.abs(_np(o) - e[:, 4 * r:4 * r + 4]).max() < 1e-5
+    # single-rank backward vs dense autograd, grad_out = ones, abs 1e-4
+    out, m, l = ra.ring_causal_attention_forward_with_stats([(q, k, v)], 0, True, 2, 3)
+    go = gpu.ones_like(q)
+    dq, dk, dv = ra.ring_causal_attention_backward([(q, k, v)], 0, [out], [m], [l], [go], True,
+                                                   2, 3)
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), np.ones((1, 8, 2, 4)))
+    for a, b in ((dq, edq), (dk, edk), (dv, edv)):
+        assert np.abs(_np(a) - b).max() < 1e-4
+
+
+def test_two_rank_python_case_on_gpu(ra, gpu):
+    """tests/test_ring_attention.py:277-321 of the reference: seed 123, T=8
+    over 2 ranks, H=2, D=4, blocks 2/2, loss = sum(out): fwd 2e-5, grads 3e-4."""
+    import torch
+
+    torch.manual_seed(123)
+    q = torch.randn(1, 8, 2, 4)
+    k = torch.randn(1, 8, 2, 4)
+    v = torch.randn(1, 8, 2, 4)
+    shards = [tuple(x[:, 4 * r:4 * r + 4].contiguous().cuda() for x in (q, k, v))
+              for r in range(2)]
+    stats = [ra.ring_causal_attention_forward_with_stats(shards, r, True, 2, 2) for r in range(2)]
+    outs, ms, ls = (list(x) for x in zip(*stats))
+    exp = dense.attention_fwd(q.numpy(), k.numpy(), v.numpy())[0]
+    edq, edk, edv = dense.attention_bwd(q.numpy(), k.numpy(), v.numpy(), np.ones((1, 8, 2, 4)))
+    gos = [gpu.ones_like(o) for o in outs]
+    for r in range(2):
+        sl = slice(4 * r, 4 * r + 4)
+        assert np.abs(_np(outs[r]) - exp[:, sl]).max() < 2e-5
+        dq, dk, dv = ra.ring_causal_attention_backward(shards, r, outs, ms, ls, gos, True, 2, 2)
+        assert np.abs(_np(dq) - edq[:, sl]).max() < 3e-4
+        assert np.abs(_np(dk) - edk[:, sl]).max() < 3e-4
+        assert np.abs(_np(dv) - edv[:, sl]).max() < 3e-4
+
+
+def test_ring_c2_shape_reduced(ra, gpu):
+    """Config 2/3 geometry (rank 7 of 8, Hq=Hkv=16, d=128, bf16) at 512
+    tokens per shard against the C restatement."""
+    rng = np.random.default_rng(2)
+    world, n, h, d = 8, 512, 16, 128
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, h, h, d, gpu.bfloat16)
+    gos = [_t(gpu, rng.standard_normal((1, n, h, d)), gpu.bfloat16) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    stats = [ra.ring_causal_attention_forward_with_stats(shards, r) for r in range(world)]
+    outs, ms, ls = (list(x) for x in zip(*stats))
+    fw, grads = _oracle_ring(qs, ks, vs, world, h, h, rank=7, gos=gos)
+    assert norm_rel(_np(outs[7]), fw[7][0]) <= BF16_TOL
+    dq, dk, dv = ra.ring_causal_attention_backward(shards, 7, outs, ms, ls, gos)
+    gpu.cuda.synchronize()
+    for a, b in zip((dq, dk, dv), grads):
+        assert norm_rel(_np(a), b) <= BF16_TOL
+
+
+def test_host_pointer_entry_points(gpu):
+    """lc_ring_fwd_with_stats_host / lc_ring_bwd_host (the CPU-tensor form a
+    candle backend binds) agree with the oracle."""
+    from longctx100m_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(4)
+    world, n, h, d = 2, 96, 2, 64
+    mk = lambda: [rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(world)]  # noqa: E731
+    qs, ks, vs, gos = mk(), mk(), mk(), mk()
+    desc = _lib.RingDesc(world, 1, 1, n, h, h, d, _lib.LC_DTYPE_F32, 0, 1, 64, 128, -1, -1)
+    out = np.zeros((1, n, h, d), np.float32)
+    m = np.zeros((1, h, n), np.float32)
+    l = np.zeros_like(m)
+    pq, _a = _lib.ptr_array([x.ctypes.data for x in qs])
+    pk, _b = _lib.ptr_array([x.ctypes.data for x in ks])
+    pv, _c = _lib.ptr_array([x.ctypes.data for x in vs])
+    _lib.check(lib.lc_ring_fwd_with_stats_host(desc, pq, pk, pv, out.ctypes.data, m.ctypes.data,
+                                               l.ctypes.data))
+    eo, em, el = ring.ring_fwd_with_stats(qs, ks, vs, 1)
+    assert norm_rel(out, eo) <= FP32_TOL and norm_rel(l, el) <= FP32_TOL
+    fw = [ring.ring_fwd_with_stats(qs, ks, vs, r) for r in range(world)]
+    outs = [x[0] for x in fw]
+    ms = [x[1] for x in fw]
+    ls = [x[2] for x in fw]
+    dq = np.zeros_like(out)
+    dk = np.zeros_like(out)
+    dv = np.zeros_like(out)
+    arrs = [_lib.ptr_array([x.ctypes.data for x in xs]) for xs in (qs, ks, vs, outs, ms, ls, gos)]
+    _lib.check(lib.lc_ring_bwd_host(desc, *[a[0] for a in arrs], dq.ctypes.data, dk.ctypes.data,
+                                    dv.ctypes.data))
+    edq, edk, edv = ring.ring_bwd(qs, ks, vs, outs, ms, ls, gos, 1)
+    for a, b in ((dq, edq), (dk, edk), (dv, edv)):
+        assert norm_rel(a, b) <= FP32_TOL
+    ref = np.zeros((1, n, h, d), np.float32)
+    _lib.check(lib.lc_reference_causal_attention_host(1, n, h, h, d, _lib.LC_DTYPE_F32,
+                                                      qs[0].ctypes.data, ks[0].ctypes.data,
+                                                      vs[0].ctypes.data, 1, -1, ref.ctypes.data))
+    assert norm_rel(ref, ring.dense(qs[0], ks[0], vs[0])) <= FP32_TOL
+
+
+def test_autograd_wrapper(ra, gpu):
+    import torch
+
+    rng = np.random.default_rng(8)
+    world, n, hq, hkv, d = 2, 128, 4, 2, 128
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, hq, hkv, d, gpu.bfloat16)
+    shards = list(zip(qs, ks, vs))
+    q = qs[1].clone().requires_grad_()
+    k = ks[1].clone().requires_grad_()
+    v = vs[1].clone().requires_grad_()
+    out = ra.RingCausalAttention.apply(q, k, v, shards, 1, True, None)
+    go = _t(gpu, rng.standard_normal((1, n, hq, d)), gpu.bfloat16)
+    out.backward(go)
+    # reference: this rank's rows of dense attention, differentiated w.r.t.
+    # this rank's q, k, v only
+    kall = np.concatenate([_np(x) for x in ks], 1)
+    vall = np.concatenate([_np(x) for x in vs], 1)
+    eo = dense.attention_fwd(_np(qs[1]), kall, vall, q_pos0=n, k_pos0=0)[0]
+    assert norm_rel(_np(out), eo) <= BF16_TOL
+    rounded = torch.tensor(eo, dtype=torch.float32).to(torch.bfloat16).float().numpy()
+    edq, edk, edv = dense.attention_bwd(_np(qs[1]), kall, vall, _np(go), q_pos0=n, k_pos0=0,
+                                        out=rounded)
+    assert norm_rel(_np(q.grad), edq) <= BF16_TOL
+    assert norm_rel(_np(k.grad), edk[:, n:]) <= BF16_TOL
+    assert norm_rel(_np(v.grad), edv[:, n:]) <= BF16_TOL
