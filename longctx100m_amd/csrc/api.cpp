@@ -98,7 +98,8 @@ int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
               float* m, float* l, hipStream_t st) {
   hipError_t e;
   if (use_mfma(p, q, k, v, nullptr))
-    e = lc::launch_fwd_mfma(p, q, k, v, o, m, l, st);
+    e = p.D == 128 ? lc::launch_fwd128(p, q, k, v, o, m, l, st)
+                   : lc::launch_fwd_mfma(p, q, k, v, o, m, l, st);
   else
     e = lc::launch_fwd_generic(p, q, k, v, o, m, l, st);
   if (e != hipSuccess) return hip_error(e, "lc_attn_fwd_shard launch");
@@ -109,14 +110,17 @@ int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
               const float* lse2, const float* delta, float* dq, float* dk, float* dv,
               hipStream_t st) {
   const bool mf = use_mfma(p, q, k, v, dout);
+  const bool d128 = p.D == 128;
   if (dq != nullptr) {
-    hipError_t e = mf ? lc::launch_bwd_dq_mfma(p, q, k, v, dout, lse2, delta, dq, st)
-                      : lc::launch_bwd_dq_generic(p, q, k, v, dout, lse2, delta, dq, st);
+    hipError_t e = !mf ? lc::launch_bwd_dq_generic(p, q, k, v, dout, lse2, delta, dq, st)
+                   : d128 ? lc::launch_dq128(p, q, k, v, dout, lse2, delta, dq, st)
+                          : lc::launch_bwd_dq_mfma(p, q, k, v, dout, lse2, delta, dq, st);
     if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dq launch");
   }
   if (dk != nullptr) {
-    hipError_t e = mf ? lc::launch_bwd_dkdv_mfma(p, q, k, v, dout, lse2, delta, dk, dv, st)
-                      : lc::launch_bwd_dkdv_generic(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    hipError_t e = !mf ? lc::launch_bwd_dkdv_generic(p, q, k, v, dout, lse2, delta, dk, dv, st)
+                   : d128 ? lc::launch_dkdv128(p, q, k, v, dout, lse2, delta, dk, dv, st)
+                          : lc::launch_bwd_dkdv_mfma(p, q, k, v, dout, lse2, delta, dk, dv, st);
     if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dk/dv launch");
   }
   return LC_OK;

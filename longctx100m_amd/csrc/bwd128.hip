@@ -1,0 +1,441 @@
+// Recomputation backward of one ring hop for head_dim 128 on bf16 MFMA
+// (gfx950 v_mfma_f32_16x16x32_bf16, fp32 accumulation).
+//
+// Semantics (rust/longctx100m-model/src/ring_attention.rs:383-409 and
+// :433-454; src/longctx100m/ring_attention.py:338-357, :373-391):
+//   P  = exp(s - m) / max(l, FLT_MIN) (0 where the row saw no key)
+//      = 2^(s*scale*log2e - lse2), lse2 from lc_attn_bwd_preprocess
+//   dS = P * (dO V^T - delta),  delta = rowsum(dO * O)
+//   dQ += dS K * scale,  dK += dS^T Q * scale,  dV += P^T dO
+//
+// Two kernels without atomics (one owner per output element per launch, so
+// results are deterministic):
+//   dq128   Q-stationary, 4 waves x 32 queries.  Q^T, dO^T in VGPRs; 64-key
+//           tiles of K and V double-buffered in LDS.
+//             S^T = K Q^T, dP^T = V dO^T   (A = K, V rows: ds_read_b128)
+//             dQ^T += K^T dS^T             (A = K^T: ds_read_b64_tr_b16)
+//   dkdv128 KV-stationary, 4 waves x 32 keys of one KV head, walking every
+//           query head of the GQA group (group sum in registers).  K^T, V^T
+//           in VGPRs; 64-query tiles of Q, dO, LSE and delta double-buffered
+//           in LDS.
+//             S = Q K^T, dP = dO V^T       (A = Q, dO rows)
+//             dV^T += dO^T P, dK^T += Q^T dS  (A = dO^T, Q^T: transposed reads)
+// Tiles are swizzled row-major and filled by direct global->LDS loads
+// (tile128.h); each score accumulator's C layout is reused as the B operand
+// of the following product.
+#include "common.h"
+#include "kernels.h"
+#include "tile128.h"
+
+namespace lc {
+namespace {
+
+constexpr int D = 128;
+constexpr int KS = D / 32;
+constexpr int DB = D / 16;
+
+struct Bwd128Args {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dout;
+  const float* lse2;
+  const float* delta;
+  float* dq;
+  float* dk;
+  float* dv;
+  int Nq, Nk, Hq, Hkv, group, n_tiles;
+  int64_t q_pos0, k_pos0, valid;
+  int causal;
+  float sl2;    // scale * log2(e)
+  float scale;  // D^-1/2
+};
+
+// ------------------------------------------------------------------- dQ --
+
+constexpr int kDqQW = 32;
+constexpr int kDqBM = 4 * kDqQW;  // queries per workgroup
+constexpr int kDqBN = 64;         // keys per tile
+constexpr int kDqTile = kDqBN * t128::kRowBytes;
+
+__global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kDqTile];  // [buf][K,V]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = a.n_tiles - 1 - (L % a.n_tiles);
+  const int bh = L / a.n_tiles;
+  const int h = bh % a.Hq;
+  const int b = bh / a.Hq;
+  const int hk = h / a.group;
+
+  const int64_t qs = (int64_t)a.Hq * D;
+  const int64_t ks = (int64_t)a.Hkv * D;
+  const uint16_t* qbase = a.q + (int64_t)b * a.Nq * qs + (int64_t)h * D;
+  const uint16_t* obase = a.dout + (int64_t)b * a.Nq * qs + (int64_t)h * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+
+  const int q0 = qt * kDqBM;
+  const int qw0 = q0 + wave * kDqQW;
+
+  const int q_end = min(q0 + kDqBM, a.Nq);
+  int64_t kend = a.Nk;
+  if (a.causal) kend = min(kend, a.q_pos0 + q_end - a.k_pos0);
+  kend = min(kend, a.valid - a.k_pos0);
+  const int ntiles = kend > 0 ? (int)((kend + kDqBN - 1) / kDqBN) : 0;
+  if (ntiles == 0) return;  // nothing visible: dQ gets no contribution
+
+  t128::load_rows<kDqBN, 4>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
+  t128::load_rows<kDqBN, 4>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+
+  bf16x8 qreg[2][KS], doreg[2][KS];
+  float lse[2], dl[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = min(qw0 + 16 * nb + c, a.Nq - 1);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      qreg[nb][kk] = *reinterpret_cast<const bf16x8*>(qbase + (int64_t)row * qs + 32 * kk + 8 * g);
+      doreg[nb][kk] = *reinterpret_cast<const bf16x8*>(obase + (int64_t)row * qs + 32 * kk + 8 * g);
+    }
+    const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
+    lse[nb] = a.lse2[si];
+    dl[nb] = a.delta[si];
+  }
+
+  int roff[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) roff[kk] = t128::row_chunk_off(c, 4 * kk + g);
+  int toff[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) toff[db] = t128::tr_off(0, 16 * db, lane);
+
+  const int64_t wq_first = a.q_pos0 + qw0;
+  const int64_t wq_last = wq_first + kDqQW - 1;
+
+  f32x4 acc[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int j = 0; j < ntiles; ++j) {
+    t128::wait_vmem();
+    __syncthreads();
+    if (j + 1 < ntiles) {
+      const int nbuf = (j + 1) & 1;
+      t128::load_rows<kDqBN, 4>(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
+      t128::load_rows<kDqBN, 4>(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
+    }
+    const int key0 = j * kDqBN;
+    const int64_t kp_first = a.k_pos0 + key0;
+    const int64_t kp_last = kp_first + kDqBN - 1;
+    if (qw0 >= a.Nq) continue;
+    if (a.causal && kp_first > wq_last) continue;
+    const bool need_mask = (a.causal && kp_last > wq_first) || kp_last >= a.valid ||
+                           key0 + kDqBN > a.Nk;
+    const uint8_t* kt = smem[j & 1][0];
+    const uint8_t* vt = smem[j & 1][1];
+
+    // Per 32-key half (kk2): S^T = K Q^T and dP^T = V dO^T for keys
+    // 32*kk2 + [16mb+4g+i], query 16nb+c; then dQ^T += K^T dS^T.
+#pragma unroll
+    for (int kk2 = 0; kk2 < kDqBN / 32; ++kk2) {
+      f32x4 s[2][2], dp[2][2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        s[mb][0] = s[mb][1] = dp[mb][0] = dp[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const int off = roff[kk] + (2 * kk2 + mb) * 16 * t128::kRowBytes;
+          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kt + off);
+          const bf16x8 va = *reinterpret_cast<const bf16x8*>(vt + off);
+          s[mb][0] = mfma16x16x32(ka, qreg[0][kk], s[mb][0]);
+          s[mb][1] = mfma16x16x32(ka, qreg[1][kk], s[mb][1]);
+          dp[mb][0] = mfma16x16x32(va, doreg[0][kk], dp[mb][0]);
+          dp[mb][1] = mfma16x16x32(va, doreg[1][kk], dp[mb][1]);
+        }
+      }
+
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int64_t qp = wq_first + 16 * nb + c;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = s[mb][nb][i];
+            if (need_mask) {
+              const int key = key0 + 32 * kk2 + 16 * mb + 4 * g + i;
+              const int64_t kp = a.k_pos0 + key;
+              if (key >= a.Nk || (a.causal && kp > qp) || kp >= a.valid) x = -INFINITY;
+            }
+            const float p = fast_exp2(fmaf(x, a.sl2, -lse[nb]));
+            s[mb][nb][i] = p * (dp[mb][nb][i] - dl[nb]);  // dS^T
+          }
+        }
+
+      const bf16x8 b0 = pack_bf16x8(s[0][0], s[1][0]);
+      const bf16x8 b1 = pack_bf16x8(s[0][1], s[1][1]);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint8_t* p = kt + toff[db] + kk2 * 32 * t128::kRowBytes;
+        const bf16x8 ka = concat_bf16x4(t128::ds_read_tr(p), t128::ds_read_tr(p + 16 * t128::kRowBytes));
+        acc[db][0] = mfma16x16x32(ka, b0, acc[db][0]);
+        acc[db][1] = mfma16x16x32(ka, b1, acc[db][1]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = qw0 + 16 * nb + c;
+    if (row < a.Nq) {
+      float* dst = a.dq + (((int64_t)b * a.Nq + row) * a.Hq + h) * D + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        f32x4* p = reinterpret_cast<f32x4*>(dst + 16 * db);
+        *p = *p + acc[db][nb] * a.scale;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dK/dV --
+
+constexpr int kKvKW = 32;
+constexpr int kKvBN = 4 * kKvKW;  // keys per workgroup
+constexpr int kKvBM = 64;         // queries per tile
+constexpr int kKvTile = kKvBM * t128::kRowBytes;
+
+__global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kKvTile];  // [buf][Q,dO]
+  __shared__ __attribute__((aligned(16))) float stat[2][2][kKvBM];        // [buf][lse2,delta]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt = L % a.n_tiles;  // early keys see the most queries: dispatched first
+  const int bh = L / a.n_tiles;
+  const int hk = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+
+  const int64_t qs = (int64_t)a.Hq * D;
+  const int64_t ks = (int64_t)a.Hkv * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+
+  const int k0 = kt * kKvBN;
+  const int kw0 = k0 + wave * kKvKW;
+
+  // Queries that can see any key of this workgroup.
+  const int64_t kp_wg_first = a.k_pos0 + k0;
+  int qstart = 0;
+  if (a.causal) {
+    const int64_t first = kp_wg_first - a.q_pos0;
+    qstart = first <= 0 ? 0 : (first >= a.Nq ? a.Nq : (int)first);
+  }
+  qstart = (qstart / kKvBM) * kKvBM;
+  const bool any_valid_key = kp_wg_first < a.valid && k0 < a.Nk;
+  const int ntq = any_valid_key ? (a.Nq - qstart + kKvBM - 1) / kKvBM : 0;
+  const int nsteps = ntq * a.group;
+  if (nsteps == 0) return;  // no visible (query, key) pair: no contribution
+
+  auto issue = [&](int step, int buf) {
+    const int hq = hk * a.group + step / ntq;
+    const int qrow0 = qstart + (step % ntq) * kKvBM;
+    const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
+    const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
+    t128::load_rows<kKvBM, 4>(qb, qs, qrow0, a.Nq, smem[buf][0], wave, lane);
+    t128::load_rows<kKvBM, 4>(ob, qs, qrow0, a.Nq, smem[buf][1], wave, lane);
+    const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.Nq;
+    if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, stat[buf][0], lane);
+    if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, stat[buf][1], lane);
+  };
+  issue(0, 0);
+
+  // K^T and V^T as B operands: lane holds key (16*nb + c), dims 32*kk + 8g .. +7.
+  bf16x8 kreg[2][KS], vreg[2][KS];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = min(kw0 + 16 * nb + c, a.Nk - 1);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      kreg[nb][kk] = *reinterpret_cast<const bf16x8*>(kbase + (int64_t)row * ks + 32 * kk + 8 * g);
+      vreg[nb][kk] = *reinterpret_cast<const bf16x8*>(vbase + (int64_t)row * ks + 32 * kk + 8 * g);
+    }
+  }
+
+  int roff[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) roff[kk] = t128::row_chunk_off(c, 4 * kk + g);
+  int toff[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) toff[db] = t128::tr_off(0, 16 * db, lane);
+
+  f32x4 dk[DB][2], dv[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+    dk[db][0] = dk[db][1] = dv[db][0] = dv[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t wk_first = a.k_pos0 + kw0;
+  const int64_t wk_last = wk_first + kKvKW - 1;
+
+  for (int step = 0; step < nsteps; ++step) {
+    t128::wait_vmem();
+    __syncthreads();
+    if (step + 1 < nsteps) issue(step + 1, (step + 1) & 1);
+    const int qrow0 = qstart + (step % ntq) * kKvBM;
+    const int64_t qp_first = a.q_pos0 + qrow0;
+    const int64_t qp_last = qp_first + kKvBM - 1;
+    if (kw0 >= a.Nk) continue;
+    if (a.causal && wk_first > qp_last) continue;
+    const bool need_mask = (a.causal && wk_last > qp_first) || wk_last >= a.valid ||
+                           kw0 + kKvKW > a.Nk || qrow0 + kKvBM > a.Nq;
+    const int buf = step & 1;
+    const uint8_t* qt_ = smem[buf][0];
+    const uint8_t* ot_ = smem[buf][1];
+
+    // Per 32-query half (kk2): S = Q K^T and dP = dO V^T for queries
+    // 32*kk2 + [16mb+4g+i], key 16nb+c; then dV^T += dO^T P, dK^T += Q^T dS.
+#pragma unroll
+    for (int kk2 = 0; kk2 < kKvBM / 32; ++kk2) {
+      f32x4 s[2][2], dp[2][2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        s[mb][0] = s[mb][1] = dp[mb][0] = dp[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const int off = roff[kk] + (2 * kk2 + mb) * 16 * t128::kRowBytes;
+          const bf16x8 qa = *reinterpret_cast<const bf16x8*>(qt_ + off);
+          const bf16x8 oa = *reinterpret_cast<const bf16x8*>(ot_ + off);
+          s[mb][0] = mfma16x16x32(qa, kreg[0][kk], s[mb][0]);
+          s[mb][1] = mfma16x16x32(qa, kreg[1][kk], s[mb][1]);
+          dp[mb][0] = mfma16x16x32(oa, vreg[0][kk], dp[mb][0]);
+          dp[mb][1] = mfma16x16x32(oa, vreg[1][kk], dp[mb][1]);
+        }
+      }
+
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int qi = 32 * kk2 + 16 * mb + 4 * g;
+        const f32x4 lse4 = *reinterpret_cast<const f32x4*>(&stat[buf][0][qi]);
+        const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][qi]);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int key = kw0 + 16 * nb + c;
+          const int64_t kp = a.k_pos0 + key;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = s[mb][nb][i];
+            if (need_mask) {
+              const int qrow = qrow0 + qi + i;
+              const int64_t qp = a.q_pos0 + qrow;
+              if (qrow >= a.Nq || key >= a.Nk || (a.causal && kp > qp) || kp >= a.valid)
+                x = -INFINITY;
+            }
+            const float p = fast_exp2(fmaf(x, a.sl2, -lse4[i]));
+            s[mb][nb][i] = p;                              // P
+            dp[mb][nb][i] = p * (dp[mb][nb][i] - dl4[i]);  // dS
+          }
+        }
+      }
+
+      const bf16x8 p0 = pack_bf16x8(s[0][0], s[1][0]);
+      const bf16x8 p1 = pack_bf16x8(s[0][1], s[1][1]);
+      const bf16x8 d0 = pack_bf16x8(dp[0][0], dp[1][0]);
+      const bf16x8 d1 = pack_bf16x8(dp[0][1], dp[1][1]);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int off = toff[db] + kk2 * 32 * t128::kRowBytes;
+        const bf16x8 oa = concat_bf16x4(t128::ds_read_tr(ot_ + off),
+                                         t128::ds_read_tr(ot_ + off + 16 * t128::kRowBytes));
+        const bf16x8 qa = concat_bf16x4(t128::ds_read_tr(qt_ + off),
+                                         t128::ds_read_tr(qt_ + off + 16 * t128::kRowBytes));
+        dv[db][0] = mfma16x16x32(oa, p0, dv[db][0]);
+        dv[db][1] = mfma16x16x32(oa, p1, dv[db][1]);
+        dk[db][0] = mfma16x16x32(qa, d0, dk[db][0]);
+        dk[db][1] = mfma16x16x32(qa, d1, dk[db][1]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = kw0 + 16 * nb + c;
+    if (row < a.Nk) {
+      const int64_t off = (((int64_t)b * a.Nk + row) * a.Hkv + hk) * D + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        f32x4* pk = reinterpret_cast<f32x4*>(a.dk + off + 16 * db);
+        f32x4* pv = reinterpret_cast<f32x4*>(a.dv + off + 16 * db);
+        *pk = *pk + dk[db][nb] * a.scale;
+        *pv = *pv + dv[db][nb];
+      }
+    }
+  }
+}
+
+Bwd128Args make_args(const Problem& p, const void* q, const void* k, const void* v,
+                     const void* dout, const float* lse2, const float* delta) {
+  Bwd128Args a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.lse2 = lse2;
+  a.delta = delta;
+  a.dq = a.dk = a.dv = nullptr;
+  a.Nq = p.Nq;
+  a.Nk = p.Nk;
+  a.Hq = p.Hq;
+  a.Hkv = p.Hkv;
+  a.group = p.Hq / p.Hkv;
+  a.n_tiles = 0;
+  a.q_pos0 = p.q_pos0;
+  a.k_pos0 = p.k_pos0;
+  a.valid = p.valid;
+  a.causal = p.causal ? 1 : 0;
+  a.sl2 = p.scale * kLog2e;
+  a.scale = p.scale;
+  return a;
+}
+
+}  // namespace
+
+hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const void* v,
+                        const void* dout, const float* lse2, const float* delta, float* dq,
+                        hipStream_t s) {
+  if (p.D != D) return hipErrorInvalidValue;
+  Bwd128Args a = make_args(p, q, k, v, dout, lse2, delta);
+  a.dq = dq;
+  a.n_tiles = (p.Nq + kDqBM - 1) / kDqBM;
+  hipLaunchKernelGGL(dq128_kernel, dim3(a.n_tiles * p.Hq * p.B), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
+                          const void* dout, const float* lse2, const float* delta, float* dk,
+                          float* dv, hipStream_t s) {
+  if (p.D != D) return hipErrorInvalidValue;
+  Bwd128Args a = make_args(p, q, k, v, dout, lse2, delta);
+  a.dk = dk;
+  a.dv = dv;
+  a.n_tiles = (p.Nk + kKvBN - 1) / kKvBN;
+  hipLaunchKernelGGL(dkdv128_kernel, dim3(a.n_tiles * p.Hkv * p.B), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace lc

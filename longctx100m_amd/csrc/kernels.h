@@ -33,6 +33,17 @@ inline int64_t key_end_for(const Problem& p, int64_t q_end) {
 // True when the bf16 MFMA kernels implement this problem.
 bool mfma_supported(const Problem& p);
 
+// head_dim 128: swizzled direct-to-LDS tiles (fwd128.hip, bwd128.hip).
+hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const void* v, float* o,
+                         float* m, float* l, hipStream_t s);
+hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const void* v,
+                        const void* dout, const float* lse2, const float* delta, float* dq,
+                        hipStream_t s);
+hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
+                          const void* dout, const float* lse2, const float* delta, float* dk,
+                          float* dv, hipStream_t s);
+
+// head_dim 64 (and 128 on request): register-staged tiles (fwd_mfma.hip, bwd_mfma.hip).
 hipError_t launch_fwd_mfma(const Problem& p, const void* q, const void* k, const void* v, float* o,
                            float* m, float* l, hipStream_t s);
 hipError_t launch_fwd_generic(const Problem& p, const void* q, const void* k, const void* v,

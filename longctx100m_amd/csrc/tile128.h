@@ -1,0 +1,95 @@
+// LDS tiles of bf16 [rows x 128] for the d=128 MFMA kernels (gfx950).
+//
+// Layout: row-major, 256 bytes per row, no padding; the sixteen 16-byte
+// chunks of row r are stored XOR-swizzled, logical chunk L at physical chunk
+// L ^ swz(r), swz(r) = 2*(r % 8) + (r % 16) / 8.  With that swizzle
+//   * a 16-lane group reading one logical chunk of 16 consecutive rows
+//     (ds_read_b128, MFMA operands whose K dimension is head_dim) touches 16
+//     distinct chunks -> all 64 banks once, and
+//   * a 32-lane half reading 2 adjacent chunks of 8 consecutive rows
+//     (ds_read_b64_tr_b16, operands whose K dimension is the row index)
+//     touches 16 distinct chunks as well.
+//
+// Tiles are filled with global_load_lds (16 bytes per lane, lane l lands at
+// base + 16*l), so one wave instruction writes 4 whole rows and staging needs
+// no VGPRs; each lane fetches the logical chunk its physical slot holds.
+//
+// Transposed operands come from the same tile through ds_read_b64_tr_b16.
+// Within a 16-lane group, output lane c slot t receives element (c % 4) of the
+// 8 bytes addressed by lane 4*t + c/4.  So if lane 4*t + q addresses row
+// (row0 + t), columns (col0 + 4q .. +3), lane c receives
+// X[row0 + t][col0 + c] for t = 0..3: the tile's columns are spread over the
+// lanes and its rows over the four slots, i.e. the MFMA operand whose M/N
+// index is the column and whose K index is the row.
+#pragma once
+
+#include "common.h"
+
+namespace lc {
+namespace t128 {
+
+constexpr int kRowBytes = 256;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int swz(int r) {
+  r &= 15;
+  return ((r & 7) << 1) | (r >> 3);
+}
+
+// Issues direct global->LDS loads of tile rows [row0, row0 + ROWS) of a
+// [*, 128] bf16 matrix (row stride `stride` elements).  Rows at or beyond
+// `nrows` re-read row nrows - 1 (finite data; callers mask those rows).
+template <int ROWS, int NW>
+__device__ __forceinline__ void load_rows(const uint16_t* base, int64_t stride, int row0,
+                                          int nrows, uint8_t* lds, int wave, int lane) {
+  static_assert(ROWS % (4 * NW) == 0, "4 rows per wave instruction");
+#pragma unroll
+  for (int i = 0; i < ROWS / (4 * NW); ++i) {
+    const int rblk = (i * NW + wave) * 4;
+    const int r = rblk + (lane >> 4);
+    const int chunk = (lane & 15) ^ swz(r);
+    int grow = row0 + r;
+    grow = grow < nrows ? grow : nrows - 1;
+    const uint16_t* g = base + (int64_t)grow * stride + chunk * 8;
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+  }
+}
+
+// Direct load of 64 consecutive fp32 values (one wave instruction).
+// Entries at or beyond n re-read entry n - 1.
+__device__ __forceinline__ void load_f32x64(const float* base, int i0, int n, float* lds,
+                                            int lane) {
+  int i = i0 + lane;
+  i = i < n ? i : n - 1;
+  __builtin_amdgcn_global_load_lds(base + i, (lds_void*)lds, 4, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Byte offset of logical chunk `chunk` of tile row `r`.
+__device__ __forceinline__ int row_chunk_off(int r, int chunk) {
+  return r * kRowBytes + 16 * (chunk ^ swz(r));
+}
+
+// Per-lane byte offset for a transposed read of columns col0..col0+15 over
+// rows row0 + 4g + t (t = slot): lane (4t + q) of group g addresses row
+// row0 + 4g + t, columns col0 + 4q .. +3.  row0 must be a multiple of 16.
+__device__ __forceinline__ int tr_off(int row0, int col0, int lane) {
+  const int g = lane >> 4;
+  const int i = lane & 15;
+  const int r = row0 + 4 * g + (i >> 2);
+  const int q = i & 3;
+  const int col = col0 + 4 * q;
+  return r * kRowBytes + 16 * ((col >> 3) ^ swz(r)) + 2 * (col & 7);
+}
+
+__device__ __forceinline__ bf16x4 ds_read_tr(const uint8_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+}  // namespace t128
+}  // namespace lc

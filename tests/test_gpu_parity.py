@@ -7,6 +7,8 @@ bf16 before it enters delta, the reference's bf16 rule
 (src/longctx100m/ring_attention.py:17,28,151,314).
 """
 
+import zlib
+
 import numpy as np
 import pytest
 
@@ -31,7 +33,7 @@ def _t(gpu, arr, dtype):
 
 
 def _np(t):
-    return t.float().cpu().numpy()
+    return t.detach().float().cpu().numpy()
 
 
 def _rand_shards(gpu, rng, world, n, hq, hkv, d, dtype, b=1):
@@ -60,7 +62,7 @@ FWD_CASES = [
 @pytest.mark.parametrize("case", FWD_CASES)
 def test_fwd_shard_bf16(ra, gpu, case, precise):
     nq, nk, hq, hkv, d, qp, kp, causal, valid = case
-    rng = np.random.default_rng(hash(case) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     q = _t(gpu, rng.standard_normal((1, nq, hq, d)), gpu.bfloat16)
     k = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.bfloat16)
     v = _t(gpu, rng.standard_normal((1, nk, hkv, d)), gpu.bfloat16)
