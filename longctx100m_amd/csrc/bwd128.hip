@@ -27,6 +27,8 @@
 #include "kernels.h"
 #include "tile128.h"
 
+#include <type_traits>
+
 namespace lc {
 namespace {
 
@@ -91,8 +93,10 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
   const int ntiles = kend > 0 ? (int)((kend + kDqBN - 1) / kDqBN) : 0;
   if (ntiles == 0) return;  // nothing visible: dQ gets no contribution
 
-  t128::load_rows<kDqBN, 4>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
-  t128::load_rows<kDqBN, 4>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+  t128::RowLoader<kDqBN, 4> ld;
+  ld.init(ks, wave, lane);
+  ld.load(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
+  ld.load(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
 
   bf16x8 qreg[2][KS], doreg[2][KS];
   float lse[2], dl[2];
@@ -123,26 +127,12 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int j = 0; j < ntiles; ++j) {
-    t128::wait_vmem();
-    __syncthreads();
-    if (j + 1 < ntiles) {
-      const int nbuf = (j + 1) & 1;
-      t128::load_rows<kDqBN, 4>(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
-      t128::load_rows<kDqBN, 4>(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
-    }
-    const int key0 = j * kDqBN;
-    const int64_t kp_first = a.k_pos0 + key0;
-    const int64_t kp_last = kp_first + kDqBN - 1;
-    if (qw0 >= a.Nq) continue;
-    if (a.causal && kp_first > wq_last) continue;
-    const bool need_mask = (a.causal && kp_last > wq_first) || kp_last >= a.valid ||
-                           key0 + kDqBN > a.Nk;
-    const uint8_t* kt = smem[j & 1][0];
-    const uint8_t* vt = smem[j & 1][1];
-
-    // Per 32-key half (kk2): S^T = K Q^T and dP^T = V dO^T for keys
-    // 32*kk2 + [16mb+4g+i], query 16nb+c; then dQ^T += K^T dS^T.
+  // One tile, per 32-key half (kk2): S^T = K Q^T and dP^T = V dO^T for keys
+  // 32*kk2 + [16mb+4g+i] x query 16nb+c, then dQ^T += K^T dS^T.  Mask (MASKED
+  // only): key k of the tile / query q of the wave are invalid when
+  // (causal && k - q > cthr) || k >= kmax.
+  auto tile = [&](auto masked_tag, const uint8_t* kt, const uint8_t* vt, int cthr, int kmax) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
     for (int kk2 = 0; kk2 < kDqBN / 32; ++kk2) {
       f32x4 s[2][2], dp[2][2];
@@ -162,25 +152,21 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
           dp[mb][1] = mfma16x16x32(va, doreg[1][kk], dp[mb][1]);
         }
       }
-
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int64_t qp = wq_first + 16 * nb + c;
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float x = s[mb][nb][i];
-            if (need_mask) {
-              const int key = key0 + 32 * kk2 + 16 * mb + 4 * g + i;
-              const int64_t kp = a.k_pos0 + key;
-              if (key >= a.Nk || (a.causal && kp > qp) || kp >= a.valid) x = -INFINITY;
+            if constexpr (MASKED) {
+              const int kr = 32 * kk2 + 16 * mb + 4 * g + i;
+              const bool bad = (a.causal && kr - (16 * nb + c) > cthr) || kr >= kmax;
+              x = bad ? -INFINITY : x;
             }
             const float p = fast_exp2(fmaf(x, a.sl2, -lse[nb]));
             s[mb][nb][i] = p * (dp[mb][nb][i] - dl[nb]);  // dS^T
           }
-        }
-
       const bf16x8 b0 = pack_bf16x8(s[0][0], s[1][0]);
       const bf16x8 b1 = pack_bf16x8(s[0][1], s[1][1]);
 #pragma unroll
@@ -190,6 +176,32 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
         acc[db][0] = mfma16x16x32(ka, b0, acc[db][0]);
         acc[db][1] = mfma16x16x32(ka, b1, acc[db][1]);
       }
+    }
+  };
+
+  for (int j = 0; j < ntiles; ++j) {
+    t128::wait_vmem();
+    __syncthreads();
+    if (j + 1 < ntiles) {
+      const int nbuf = (j + 1) & 1;
+      ld.load(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
+      ld.load(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
+    }
+    const int key0 = j * kDqBN;
+    const int64_t kp_first = a.k_pos0 + key0;
+    const int64_t kp_last = kp_first + kDqBN - 1;
+    if (qw0 >= a.Nq) continue;
+    if (a.causal && kp_first > wq_last) continue;
+    const uint8_t* kt = smem[j & 1][0];
+    const uint8_t* vt = smem[j & 1][1];
+    if ((a.causal && kp_last > wq_first) || kp_last >= a.valid || key0 + kDqBN > a.Nk) {
+      const int64_t ct = wq_first - kp_first;
+      const int cthr = (int)(ct < -4096 ? -4096 : (ct > 4096 ? 4096 : ct));
+      const int64_t km = min((int64_t)(a.Nk - key0), a.valid - kp_first);
+      const int kmax = (int)(km < 0 ? 0 : (km > kDqBN ? kDqBN : km));
+      tile(std::true_type{}, kt, vt, cthr, kmax);
+    } else {
+      tile(std::false_type{}, kt, vt, 0, kDqBN);
     }
   }
 
@@ -211,12 +223,13 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 
 constexpr int kKvKW = 32;
 constexpr int kKvBN = 4 * kKvKW;  // keys per workgroup
-constexpr int kKvBM = 64;         // queries per tile
+constexpr int kKvBM = 32;         // queries per tile
 constexpr int kKvTile = kKvBM * t128::kRowBytes;
 
-__global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
+__global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kKvTile];  // [buf][Q,dO]
-  __shared__ __attribute__((aligned(16))) float stat[2][2][kKvBM];        // [buf][lse2,delta]
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kKvBN * t128::kRowBytes];
+  __shared__ __attribute__((aligned(16))) float stat[2][2][64];           // [buf][lse2,delta]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -251,34 +264,43 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
   const int nsteps = ntq * a.group;
   if (nsteps == 0) return;  // no visible (query, key) pair: no contribution
 
+  t128::RowLoader<kKvBM, 4> ld;
+  ld.init(qs, wave, lane);
   auto issue = [&](int step, int buf) {
     const int hq = hk * a.group + step / ntq;
     const int qrow0 = qstart + (step % ntq) * kKvBM;
     const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
     const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
-    t128::load_rows<kKvBM, 4>(qb, qs, qrow0, a.Nq, smem[buf][0], wave, lane);
-    t128::load_rows<kKvBM, 4>(ob, qs, qrow0, a.Nq, smem[buf][1], wave, lane);
+    ld.load(qb, qs, qrow0, a.Nq, smem[buf][0], wave, lane);
+    ld.load(ob, qs, qrow0, a.Nq, smem[buf][1], wave, lane);
     const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.Nq;
     if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, stat[buf][0], lane);
     if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, stat[buf][1], lane);
+    // (64 entries are fetched; the tile uses the first kKvBM)
   };
   issue(0, 0);
 
-  // K^T and V^T as B operands: lane holds key (16*nb + c), dims 32*kk + 8g .. +7.
-  bf16x8 kreg[2][KS], vreg[2][KS];
+  // K^T as B operand in VGPRs: lane holds key (16*nb + c), dims 32*kk + 8g .. +7.
+  // V^T, the B operand of dP, is read from an LDS tile of the workgroup's
+  // keys (keeps the kernel within 256 VGPRs, i.e. two workgroups per CU).
+  bf16x8 kreg[2][KS];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int row = min(kw0 + 16 * nb + c, a.Nk - 1);
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
+    for (int kk = 0; kk < KS; ++kk)
       kreg[nb][kk] = *reinterpret_cast<const bf16x8*>(kbase + (int64_t)row * ks + 32 * kk + 8 * g);
-      vreg[nb][kk] = *reinterpret_cast<const bf16x8*>(vbase + (int64_t)row * ks + 32 * kk + 8 * g);
-    }
+  }
+  {
+    t128::RowLoader<kKvBN, 4> vld;
+    vld.init(ks, wave, lane);
+    vld.load(vbase, ks, k0, a.Nk, v_lds, wave, lane);
   }
 
   int roff[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) roff[kk] = t128::row_chunk_off(c, 4 * kk + g);
+  const int* voff = roff;  // V^T rows of the V tile: same (row c, chunk 4kk+g) map
   int toff[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) toff[db] = t128::tr_off(0, 16 * db, lane);
@@ -291,23 +313,21 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
   const int64_t wk_first = a.k_pos0 + kw0;
   const int64_t wk_last = wk_first + kKvKW - 1;
 
-  for (int step = 0; step < nsteps; ++step) {
-    t128::wait_vmem();
-    __syncthreads();
-    if (step + 1 < nsteps) issue(step + 1, (step + 1) & 1);
-    const int qrow0 = qstart + (step % ntq) * kKvBM;
-    const int64_t qp_first = a.q_pos0 + qrow0;
-    const int64_t qp_last = qp_first + kKvBM - 1;
-    if (kw0 >= a.Nk) continue;
-    if (a.causal && wk_first > qp_last) continue;
-    const bool need_mask = (a.causal && wk_last > qp_first) || wk_last >= a.valid ||
-                           kw0 + kKvKW > a.Nk || qrow0 + kKvBM > a.Nq;
-    const int buf = step & 1;
+  // One query tile, per 32-query half (kk2): S = Q K^T and dP = dO V^T for
+  // queries 32*kk2 + [16mb+4g+i] x key 16nb+c of the wave, then
+  // dV^T += dO^T P and dK^T += Q^T dS.  Mask (MASKED only): query q of the
+  // tile / key k of the wave are invalid when
+  // (causal && k - q > cthr) || k >= kmax || q >= qmax.
+  auto tile = [&](auto masked_tag, int buf, int cthr, int kmax, int qmax) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     const uint8_t* qt_ = smem[buf][0];
     const uint8_t* ot_ = smem[buf][1];
-
-    // Per 32-query half (kk2): S = Q K^T and dP = dO V^T for queries
-    // 32*kk2 + [16mb+4g+i], key 16nb+c; then dV^T += dO^T P, dK^T += Q^T dS.
+    bf16x8 vb[2][KS];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk)
+        vb[nb][kk] = *reinterpret_cast<const bf16x8*>(v_lds + voff[kk] + (wave * 2 + nb) * 16 * t128::kRowBytes);
 #pragma unroll
     for (int kk2 = 0; kk2 < kKvBM / 32; ++kk2) {
       f32x4 s[2][2], dp[2][2];
@@ -323,11 +343,10 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
           const bf16x8 oa = *reinterpret_cast<const bf16x8*>(ot_ + off);
           s[mb][0] = mfma16x16x32(qa, kreg[0][kk], s[mb][0]);
           s[mb][1] = mfma16x16x32(qa, kreg[1][kk], s[mb][1]);
-          dp[mb][0] = mfma16x16x32(oa, vreg[0][kk], dp[mb][0]);
-          dp[mb][1] = mfma16x16x32(oa, vreg[1][kk], dp[mb][1]);
+          dp[mb][0] = mfma16x16x32(oa, vb[0][kk], dp[mb][0]);
+          dp[mb][1] = mfma16x16x32(oa, vb[1][kk], dp[mb][1]);
         }
       }
-
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         const int qi = 32 * kk2 + 16 * mb + 4 * g;
@@ -335,16 +354,13 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
         const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][qi]);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          const int key = kw0 + 16 * nb + c;
-          const int64_t kp = a.k_pos0 + key;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float x = s[mb][nb][i];
-            if (need_mask) {
-              const int qrow = qrow0 + qi + i;
-              const int64_t qp = a.q_pos0 + qrow;
-              if (qrow >= a.Nq || key >= a.Nk || (a.causal && kp > qp) || kp >= a.valid)
-                x = -INFINITY;
+            if constexpr (MASKED) {
+              const int kr = 16 * nb + c;
+              const bool bad = (a.causal && kr - (qi + i) > cthr) || kr >= kmax || qi + i >= qmax;
+              x = bad ? -INFINITY : x;
             }
             const float p = fast_exp2(fmaf(x, a.sl2, -lse4[i]));
             s[mb][nb][i] = p;                              // P
@@ -352,7 +368,6 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
           }
         }
       }
-
       const bf16x8 p0 = pack_bf16x8(s[0][0], s[1][0]);
       const bf16x8 p1 = pack_bf16x8(s[0][1], s[1][1]);
       const bf16x8 d0 = pack_bf16x8(dp[0][0], dp[1][0]);
@@ -369,6 +384,29 @@ __global__ __launch_bounds__(256, 1) void dkdv128_kernel(Bwd128Args a) {
         dk[db][0] = mfma16x16x32(qa, d0, dk[db][0]);
         dk[db][1] = mfma16x16x32(qa, d1, dk[db][1]);
       }
+    }
+  };
+
+  for (int step = 0; step < nsteps; ++step) {
+    t128::wait_vmem();
+    __syncthreads();
+    if (step + 1 < nsteps) issue(step + 1, (step + 1) & 1);
+    const int qrow0 = qstart + (step % ntq) * kKvBM;
+    const int64_t qp_first = a.q_pos0 + qrow0;
+    const int64_t qp_last = qp_first + kKvBM - 1;
+    if (kw0 >= a.Nk) continue;
+    if (a.causal && wk_first > qp_last) continue;
+    const int buf = step & 1;
+    if ((a.causal && wk_last > qp_first) || wk_last >= a.valid || kw0 + kKvKW > a.Nk ||
+        qrow0 + kKvBM > a.Nq) {
+      const int64_t ct = qp_first - wk_first;
+      const int cthr = (int)(ct < -4096 ? -4096 : (ct > 4096 ? 4096 : ct));
+      const int64_t km = min((int64_t)(a.Nk - kw0), a.valid - wk_first);
+      const int kmax = (int)(km < 0 ? 0 : (km > kKvKW ? kKvKW : km));
+      const int qmax = min(a.Nq - qrow0, kKvBM);
+      tile(std::true_type{}, buf, cthr, kmax, qmax);
+    } else {
+      tile(std::false_type{}, buf, 0, kKvKW, kKvBM);
     }
   }
 

@@ -17,11 +17,21 @@
 // Computing S^T puts each lane's scores in a single query column (query =
 // lane % 16): the row max is per-lane plus two cross-lane steps, the row sum
 // stays lane-partial until the epilogue.  The mask is applied only on tiles
-// that straddle the diagonal, valid_length or the shard tail.  GQA: query
-// head h reads KV head h / (Hq / Hkv).
+// that straddle the diagonal, valid_length or the shard tail (a separate,
+// branch-free instantiation of the tile body).  GQA: query head h reads KV
+// head h / (Hq / Hkv).
+//
+// Lazy rescaling: a row's reference maximum (log2 domain) is only raised when
+// a tile's maximum exceeds it by more than kRescaleSlack, so the O^T *= alpha
+// pass is skipped on almost every tile (p stays <= 2^kRescaleSlack, exact in
+// the fp32 accumulators).  The true row maximum is tracked separately and the
+// epilogue converts l to it, so m and l are exactly the reference's
+// statistics (max of the masked scaled scores and sum exp(s - m)).
 #include "common.h"
 #include "kernels.h"
 #include "tile128.h"
+
+#include <type_traits>
 
 namespace lc {
 namespace {
@@ -34,6 +44,7 @@ constexpr int BN = 64;              // keys per tile
 constexpr int KS = D / 32;          // MFMA k-steps over head_dim
 constexpr int DB = D / 16;          // 16-wide head_dim blocks
 constexpr int kTileBytes = BN * t128::kRowBytes;
+constexpr float kRescaleSlack = 8.0f;  // log2 units
 
 struct Fwd128Args {
   const uint16_t* q;
@@ -79,9 +90,11 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   kend = min(kend, a.valid - a.k_pos0);
   const int ntiles = kend > 0 ? (int)((kend + BN - 1) / BN) : 0;
 
+  t128::RowLoader<BN, kWaves> ld;
+  ld.init(ks, wave, lane);
   if (ntiles > 0) {
-    t128::load_rows<BN, kWaves>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
-    t128::load_rows<BN, kWaves>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+    ld.load(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
+    ld.load(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
   }
 
   // Q^T operand: lane holds query 16*nb + c, head dims 32*kk + 8g .. +7.
@@ -108,28 +121,17 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   f32x4 o[DB][2];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db][0] = o[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mrun[2] = {-INFINITY, -INFINITY};
+  float mrun[2] = {-INFINITY, -INFINITY};   // reference maximum of p (log2 units)
+  float mtrue[2] = {-INFINITY, -INFINITY};  // exact running maximum (log2 units)
   float lsum[2] = {0.f, 0.f};
 
-  for (int j = 0; j < ntiles; ++j) {
-    t128::wait_vmem();
-    __syncthreads();
-    if (j + 1 < ntiles) {
-      const int nb_ = (j + 1) & 1;
-      t128::load_rows<BN, kWaves>(kbase, ks, (j + 1) * BN, a.Nk, smem[nb_][0], wave, lane);
-      t128::load_rows<BN, kWaves>(vbase, ks, (j + 1) * BN, a.Nk, smem[nb_][1], wave, lane);
-    }
-    const int key0 = j * BN;
-    const int64_t kp_first = a.k_pos0 + key0;
-    const int64_t kp_last = kp_first + BN - 1;
-    if (qw0 >= a.Nq) continue;                     // wave past the shard tail
-    if (a.causal && kp_first > wq_last) continue;  // every key after every query
-    const bool need_mask = (a.causal && kp_last > wq_first) || kp_last >= a.valid ||
-                           key0 + BN > a.Nk;
-    const uint8_t* kt = smem[j & 1][0];
-    const uint8_t* vt = smem[j & 1][1];
-
-    // S^T = K Q^T : s[mb][nb][i] = S^T[key 16mb+4g+i][query 16nb+c]
+  // One tile: S^T = K Q^T, mask (MASKED only), online softmax, O^T += V^T P^T.
+  // For the mask, key k of the tile and query column q of the wave are
+  // invalid when (causal && k - q > cthr) || k >= kmax, with
+  // cthr = (q_pos0 + qw0) - (k_pos0 + key0) and kmax the first key index past
+  // Nk / valid_length, both relative to the tile.
+  auto tile = [&](auto masked_tag, const uint8_t* kt, const uint8_t* vt, int cthr, int kmax) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     f32x4 s[4][2];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) s[mb][0] = s[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -142,23 +144,18 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
         s[mb][1] = mfma16x16x32(ka, qreg[1][kk], s[mb][1]);
       }
     }
-
-    if (need_mask) {
+    if constexpr (MASKED) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int64_t qp = wq_first + 16 * nb + c;
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 16 * mb + 4 * g + i;
-            const int64_t kp = a.k_pos0 + key;
-            if (key >= a.Nk || (a.causal && kp > qp) || kp >= a.valid) s[mb][nb][i] = -INFINITY;
+            const int kr = 16 * mb + 4 * g + i;
+            const bool bad = (a.causal && kr - (16 * nb + c) > cthr) || kr >= kmax;
+            s[mb][nb][i] = bad ? -INFINITY : s[mb][nb][i];
           }
-        }
     }
-
-    // Online softmax in the log2 domain: p = 2^(s*scale*log2e - m2).
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       float mx = s[0][nb][0];
@@ -166,14 +163,18 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mb][nb][i]);
-      mx = group4_max(mx);
-      const float mnew = fmaxf(mrun[nb], mx * a.sl2);
-      const float muse = (mnew == -INFINITY) ? 0.f : mnew;  // no key yet: p = alpha = 0
-      const float alpha = fast_exp2(mrun[nb] - muse);
-      mrun[nb] = mnew;
-      lsum[nb] *= alpha;
+      mx = group4_max(mx) * a.sl2;
+      mtrue[nb] = fmaxf(mtrue[nb], mx);
+      const bool raise = mx > mrun[nb] + kRescaleSlack;
+      if (__any(raise)) {
+        const float mnew = raise ? mx : mrun[nb];
+        const float alpha = raise ? fast_exp2(mrun[nb] - mnew) : 1.f;  // mrun = -inf: 0
+        mrun[nb] = mnew;
+        lsum[nb] *= alpha;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) o[db][nb] *= alpha;
+        for (int db = 0; db < DB; ++db) o[db][nb] *= alpha;
+      }
+      const float muse = (mrun[nb] == -INFINITY) ? 0.f : mrun[nb];  // no key yet: p = 0
       float ps = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
@@ -185,8 +186,6 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
         }
       lsum[nb] += ps;
     }
-
-    // O^T += V^T P^T over the tile's two 32-key steps.
 #pragma unroll
     for (int kk = 0; kk < BN / 32; ++kk) {
       const bf16x8 pb0 = pack_bf16x8(s[2 * kk][0], s[2 * kk + 1][0]);
@@ -199,23 +198,50 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
         o[db][1] = mfma16x16x32(va, pb1, o[db][1]);
       }
     }
+  };
+
+  for (int j = 0; j < ntiles; ++j) {
+    t128::wait_vmem();
+    __syncthreads();
+    if (j + 1 < ntiles) {
+      const int nbuf = (j + 1) & 1;
+      ld.load(kbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][0], wave, lane);
+      ld.load(vbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][1], wave, lane);
+    }
+    const int key0 = j * BN;
+    const int64_t kp_first = a.k_pos0 + key0;
+    const int64_t kp_last = kp_first + BN - 1;
+    if (qw0 >= a.Nq) continue;                     // wave past the shard tail
+    if (a.causal && kp_first > wq_last) continue;  // every key after every query
+    const uint8_t* kt = smem[j & 1][0];
+    const uint8_t* vt = smem[j & 1][1];
+    if ((a.causal && kp_last > wq_first) || kp_last >= a.valid || key0 + BN > a.Nk) {
+      const int64_t ct = wq_first - kp_first;
+      const int cthr = (int)(ct < -4096 ? -4096 : (ct > 4096 ? 4096 : ct));
+      const int64_t km = min((int64_t)(a.Nk - key0), a.valid - kp_first);
+      const int kmax = (int)(km < 0 ? 0 : (km > BN ? BN : km));
+      tile(std::true_type{}, kt, vt, cthr, kmax);
+    } else {
+      tile(std::false_type{}, kt, vt, 0, BN);
+    }
   }
 
   // Epilogue: o = acc / l; m in natural-log units; l as the reference defines it.
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const float lt = group4_sum(lsum[nb]);
+    const float lt = group4_sum(lsum[nb]);  // relative to mrun
     const int row = qw0 + 16 * nb + c;
     if (row < a.Nq) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const float ltrue = lt > 0.f ? lt * fast_exp2(mrun[nb] - mtrue[nb]) : 0.f;
       float* orow = a.o + (((int64_t)b * a.Nq + row) * a.Hq + h) * D;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db][nb] * inv;
       if (g == 0) {
         const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
-        a.m[si] = (mrun[nb] == -INFINITY) ? -INFINITY : mrun[nb] * kLn2;
-        a.l[si] = lt;
+        a.m[si] = (mtrue[nb] == -INFINITY) ? -INFINITY : mtrue[nb] * kLn2;
+        a.l[si] = ltrue;
       }
     }
   }

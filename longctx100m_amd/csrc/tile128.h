@@ -39,24 +39,49 @@ __device__ __forceinline__ int swz(int r) {
   return ((r & 7) << 1) | (r >> 3);
 }
 
-// Issues direct global->LDS loads of tile rows [row0, row0 + ROWS) of a
-// [*, 128] bf16 matrix (row stride `stride` elements).  Rows at or beyond
-// `nrows` re-read row nrows - 1 (finite data; callers mask those rows).
+// Direct global->LDS loader for tiles of ROWS rows of a [*, 128] bf16
+// matrix (row stride `stride` elements), NW waves, one wave instruction per
+// 4 rows.  The per-lane byte offsets inside a tile are computed once; a tile
+// that lies fully inside the matrix is issued from a uniform base pointer
+// plus those offsets, the last (partial) tile re-reads row nrows - 1 for
+// rows past the end (finite data; callers mask those rows).
 template <int ROWS, int NW>
-__device__ __forceinline__ void load_rows(const uint16_t* base, int64_t stride, int row0,
-                                          int nrows, uint8_t* lds, int wave, int lane) {
+struct RowLoader {
   static_assert(ROWS % (4 * NW) == 0, "4 rows per wave instruction");
+  static constexpr int kInst = ROWS / (4 * NW);
+  uint32_t off[kInst];  // byte offset of this lane's 16-byte chunk within a tile
+
+  __device__ __forceinline__ void init(int64_t stride, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < ROWS / (4 * NW); ++i) {
-    const int rblk = (i * NW + wave) * 4;
-    const int r = rblk + (lane >> 4);
-    const int chunk = (lane & 15) ^ swz(r);
-    int grow = row0 + r;
-    grow = grow < nrows ? grow : nrows - 1;
-    const uint16_t* g = base + (int64_t)grow * stride + chunk * 8;
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+    for (int i = 0; i < kInst; ++i) {
+      const int r = (i * NW + wave) * 4 + (lane >> 4);
+      off[i] = (uint32_t)(r * stride * 2 + 16 * ((lane & 15) ^ swz(r)));
+    }
   }
-}
+
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int row0, int nrows,
+                                       uint8_t* lds, int wave, int lane) const {
+    if (row0 + ROWS <= nrows) {
+      const uint8_t* tb = reinterpret_cast<const uint8_t*>(base + (int64_t)row0 * stride);
+#pragma unroll
+      for (int i = 0; i < kInst; ++i)
+        __builtin_amdgcn_global_load_lds(tb + off[i],
+                                         (lds_void*)(lds + (i * NW + wave) * 4 * kRowBytes), 16,
+                                         0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int rblk = (i * NW + wave) * 4;
+        const int r = rblk + (lane >> 4);
+        const int chunk = (lane & 15) ^ swz(r);
+        int grow = row0 + r;
+        grow = grow < nrows ? grow : nrows - 1;
+        const uint16_t* g = base + (int64_t)grow * stride + chunk * 8;
+        __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+      }
+    }
+  }
+};
 
 // Direct load of 64 consecutive fp32 values (one wave instruction).
 // Entries at or beyond n re-read entry n - 1.
