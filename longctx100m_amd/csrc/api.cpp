@@ -17,7 +17,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/longctx100m_attn.h"
+#include "longctx100m_attn.h"
 #include "kernels.h"
 
 namespace {

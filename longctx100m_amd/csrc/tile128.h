@@ -2,13 +2,17 @@
 //
 // Layout: row-major, 256 bytes per row, no padding; the sixteen 16-byte
 // chunks of row r are stored XOR-swizzled, logical chunk L at physical chunk
-// L ^ swz(r), swz(r) = 2*(r % 8) + (r % 16) / 8.  With that swizzle
-//   * a 16-lane group reading one logical chunk of 16 consecutive rows
-//     (ds_read_b128, MFMA operands whose K dimension is head_dim) touches 16
-//     distinct chunks -> all 64 banks once, and
-//   * a 32-lane half reading 2 adjacent chunks of 8 consecutive rows
-//     (ds_read_b64_tr_b16, operands whose K dimension is the row index)
-//     touches 16 distinct chunks as well.
+// L ^ swz(r).  gfx950's LDS has 64 banks of 4 bytes (256 bytes per cycle) and,
+// as measured with the SQ_LDS_BANK_CONFLICT counter:
+//   * ds_read_b128 serves 16 lanes per cycle, grouped by quads (4 lanes) with
+//     the quad index of equal parity: lanes {0-3, 12-15, 20-27} together,
+//     {4-11, 16-19, 28-31} together, and likewise in lanes 32-63;
+//   * ds_read_b64_tr_b16 serves lanes 0-31 and lanes 32-63 in separate cycles.
+// The MFMA reads of this file are: row reads (lane c of group g reads row c,
+// logical chunk 4kk + g) and transposed reads (lanes of group g read rows
+// 4g..4g+3, 32 bytes each, a chunk pair 2db, 2db+1).  swz maps rows 0-7 to
+// chunks 0,2,..,14, rows 8-11 to 9,11,13,15 and rows 12-15 to 1,3,5,7, which
+// makes every cycle of both patterns touch 16 distinct chunks (no conflicts).
 //
 // Tiles are filled with global_load_lds (16 bytes per lane, lane l lands at
 // base + 16*l), so one wave instruction writes 4 whole rows and staging needs
@@ -36,7 +40,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int swz(int r) {
   r &= 15;
-  return ((r & 7) << 1) | (r >> 3);
+  return (((r + 4 * (r >> 3)) & 7) << 1) | (r >> 3);
 }
 
 // Direct global->LDS loader for tiles of ROWS rows of a [*, 128] bf16
