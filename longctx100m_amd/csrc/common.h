@@ -78,17 +78,29 @@ __device__ __forceinline__ bf16x8 concat_bf16x4(const bf16x4& lo, const bf16x4& 
   return r;
 }
 
-// Max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
-__device__ __forceinline__ float group4_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  x = fmaxf(x, __shfl_xor(x, 32, 64));
-  return x;
+// Max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48),
+// with gfx950's v_permlane32_swap / v_permlane16_swap (no LDS round trip):
+// swap(x, x) returns (x with its upper half replaced by the lower, x with its
+// lower half replaced by the upper), so combining the pair combines l and
+// l ^ 32 (resp. l ^ 16).
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
-__device__ __forceinline__ float group4_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float group4_max(float x) { return xor16_max(xor32_max(x)); }
+__device__ __forceinline__ float group4_sum(float x) { return xor16_sum(xor32_sum(x)); }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup p runs on
 // XCD p % 8).  Give every XCD a contiguous range of logical tile ids so the
