@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--long-shard", action="store_true",
+                    help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
+                         "against its diagonal block plus one full incoming 1M-token KV shard; "
+                         "prints its own JSON line with TFLOP/s and the HBM footprint")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -126,6 +130,63 @@ def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
     return sum(per[k] for k in names) if names else None
 
 
+def long_shard(args, torch, ra) -> int:
+    """rank 1 of a 2-shard layout with 1,000,000 local tokens,
+    Hq = Hkv = 16, d = 128, bf16; forward over the diagonal block and one full
+    incoming shard, merged by LSE (1M mod 128 = 64, so every kernel runs tail tiles)."""
+    n, h, d = 1_000_000, 16, 128
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    bf = torch.bfloat16
+    torch.cuda.reset_peak_memory_stats()
+    randn = lambda *s: torch.randn(*s, generator=gen, device=dev, dtype=torch.float32).to(bf)  # noqa: E731
+    log(f"long shard: n={n} H={h} d={d} bf16, diagonal + 1 full shard")
+    q = randn(1, n, h, d)
+    k = [randn(1, n, h, d) for _ in range(2)]
+    v = [randn(1, n, h, d) for _ in range(2)]
+    f32 = dict(device=dev, dtype=torch.float32)
+    o_run, o_part = torch.empty(1, n, h, d, **f32), torch.empty(1, n, h, d, **f32)
+    m, l, m2, l2 = (torch.empty(1, h, n, **f32) for _ in range(4))
+    out = torch.empty(1, n, h, d, device=dev, dtype=bf)
+
+    def step():
+        ra.fwd_shard(q, k[1], v[1], q_pos0=n, k_pos0=n, o=o_run, m=m, l=l)      # diagonal
+        ra.fwd_shard(q, k[0], v[0], q_pos0=n, k_pos0=0, o=o_part, m=m2, l=l2)   # full
+        ra.merge(o_run, m, l, o_part, m2, l2, out=out)
+
+    steps = max(1, min(args.steps, 2))
+    for _ in range(max(0, min(args.warmup, 1))):
+        step()
+    torch.cuda.synchronize()
+    log("long shard: warmup done")
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    flops = 1.5 * 4.0 * n * n * h * d
+    resident = sum(x.numel() * x.element_size() for x in (q, *k, *v, o_run, o_part, m, l, m2, l2, out))
+    line = {
+        "metric": "causal attn fwd TFLOP/s @1M-token bf16 shard (diagonal + 1 full shard)",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": steps, "ms_per_step": round(ms, 2), "higher_is_better": True,
+        "pct_mfma_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "dtype": "bf16", "data": "synthetic: Q, K, V ~ N(0,1), seeded",
+        "config": {"workload": "BASELINE config 5: 1,000,000 local tokens, Hq=Hkv=16, d=128, "
+                               "diagonal + 1 full incoming 1M-token KV shard, LSE merge",
+                   "local_tokens": n, "heads_q": h, "heads_kv": h, "head_dim": d},
+        "flops_per_step": flops,
+        "hbm_footprint_gb": {"resident_tensors": round(resident / 1e9, 3),
+                             "torch_peak_allocated": round(torch.cuda.max_memory_allocated() / 1e9, 3)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -145,6 +206,9 @@ def main() -> int:
         return 0
 
     from longctx100m_amd import ring_attention as ra
+
+    if args.long_shard:
+        return long_shard(args, torch, ra)
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")

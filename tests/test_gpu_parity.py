@@ -350,3 +350,77 @@ def test_autograd_wrapper(ra, gpu):
     assert norm_rel(_np(q.grad), edq) <= BF16_TOL
     assert norm_rel(_np(k.grad), edk[:, n:]) <= BF16_TOL
     assert norm_rel(_np(v.grad), edv[:, n:]) <= BF16_TOL
+
+
+def test_full_size_c2_c3_spot_check(ra, gpu):
+    """BASELINE configs 2/3 at full size (rank 7 of 8, 32768-token bf16 shards,
+    Hq=Hkv=16, d=128) through the ring entry points.  Sampled output rows,
+    statistics, dQ rows and dK/dV keys are recomputed independently in fp32
+    over all 8 x 32768 keys (torch on the GPU) and must agree within the bf16
+    bar."""
+    torch = gpu
+    world, rank, n, h, d = 8, 7, 32768, 16, 128
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    rnd = lambda *s: torch.randn(*s, generator=gen, device="cuda").to(torch.bfloat16)  # noqa: E731
+    q = rnd(1, n, h, d)
+    ks = [rnd(1, n, h, d) for _ in range(world)]
+    vs = [rnd(1, n, h, d) for _ in range(world)]
+    dout = rnd(1, n, h, d)
+    shards = [(q, ks[r], vs[r]) for r in range(world)]  # only rank 7's Q is read
+    out, m, l = ra.ring_causal_attention_forward_with_stats(shards, rank)
+    dq, dk, dv = ra.ring_causal_attention_backward(shards, rank, [out] * world, [m] * world,
+                                                   [l] * world, [dout] * world)
+    torch.cuda.synchronize()
+    scale = d ** -0.5
+    kall = torch.cat(ks, 1)[0].float()  # [world*n, h, d]
+    vall = torch.cat(vs, 1)[0].float()
+    q0, o0, do0 = q[0].float(), out[0].float(), dout[0].float()
+    rows = [0, 1, 4097, 16384, 32766, 32767] + torch.randint(0, n, (6,), generator=gen, device="cuda").tolist()
+    heads = [0, 11]
+    errs = {"out": [], "dq": [], "m": [], "l": []}
+    refs = {"out": [], "dq": []}
+    for hh in heads:
+        for r in rows:
+            kv = kall[: rank * n + r + 1, hh]  # causal: keys up to the query's position
+            vv = vall[: rank * n + r + 1, hh]
+            s = (kv @ q0[r, hh]) * scale
+            mx = s.max()
+            p = torch.exp(s - mx)
+            lsum = p.sum()
+            ref_o = (p / lsum) @ vv
+            errs["m"].append(abs(float(m[0, hh, r, 0]) - float(mx)) / max(1.0, abs(float(mx))))
+            errs["l"].append(abs(float(l[0, hh, r, 0]) - float(lsum)) / float(lsum))
+            errs["out"].append(float((o0[r, hh] - ref_o).abs().max()))
+            refs["out"].append(float(ref_o.abs().max()))
+            delta = float((do0[r, hh] * o0[r, hh]).sum())
+            pn = p / lsum
+            ds = pn * (vv @ do0[r, hh] - delta)
+            ref_dq = (ds @ kv) * scale
+            errs["dq"].append(float((dq[0, r, hh].float() - ref_dq).abs().max()))
+            refs["dq"].append(float(ref_dq.abs().max()))
+    assert max(errs["out"]) / max(refs["out"]) <= 2e-2
+    assert max(errs["dq"]) / max(refs["dq"]) <= 2e-2
+    assert max(errs["m"]) <= 1e-4 and max(errs["l"]) <= 1e-3
+    # dK / dV of sampled keys of this rank's own shard (pass 1 of the reference backward):
+    # contributions of every query i of the shard with i >= key.
+    lse = (m[0, :, :, 0] + torch.log(l[0, :, :, 0])).float()  # [h, n]
+    delta_all = (do0 * o0).sum(-1)  # [n, h]
+    kerr, kref, verr, vref = [], [], [], []
+    for hh in heads:
+        for j in [0, 5, 4096, 20000, 32767]:
+            kj = ks[rank][0, j, hh].float()
+            vj = vs[rank][0, j, hh].float()
+            qi = q0[j:, hh]
+            s = (qi @ kj) * scale
+            p = torch.exp(s - lse[hh, j:])
+            dsj = p * (do0[j:, hh] @ vj - delta_all[j:, hh])
+            ref_dk = (dsj @ qi) * scale
+            ref_dv = p @ do0[j:, hh]
+            kerr.append(float((dk[0, j, hh].float() - ref_dk).abs().max()))
+            kref.append(float(ref_dk.abs().max()))
+            verr.append(float((dv[0, j, hh].float() - ref_dv).abs().max()))
+            vref.append(float(ref_dv.abs().max()))
+    assert max(kerr) / max(kref) <= 2e-2
+    assert max(verr) / max(vref) <= 2e-2
+    assert torch.isfinite(out.float()).all() and torch.isfinite(dq.float()).all()
