@@ -266,9 +266,10 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
 
   t128::RowLoader<kKvBM, 4> ld;
   ld.init(qs, wave, lane);
-  auto issue = [&](int step, int buf) {
-    const int hq = hk * a.group + step / ntq;
-    const int qrow0 = qstart + (step % ntq) * kKvBM;
+  // Steps walk (query head of the group, query tile) with running counters
+  // (no integer division per step): step s covers head hk*group + s / ntq and
+  // query rows qstart + (s % ntq) * kKvBM.
+  auto issue = [&](int hq, int qrow0, int buf) {
     const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
     const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
     ld.load(qb, qs, qrow0, a.Nq, smem[buf][0], wave, lane);
@@ -278,7 +279,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, stat[buf][1], lane);
     // (64 entries are fetched; the tile uses the first kKvBM)
   };
-  issue(0, 0);
+  const int hq0 = hk * a.group;
+  issue(hq0, qstart, 0);
 
   // K^T as B operand in VGPRs: lane holds key (16*nb + c), dims 32*kk + 8g .. +7.
   // V^T, the B operand of dP, is read from an LDS tile of the workgroup's
@@ -387,11 +389,20 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     }
   };
 
+  int cur_q = qstart;                  // step being computed
+  int nxt_hq = hq0, nxt_q = qstart;    // step being prefetched
   for (int step = 0; step < nsteps; ++step) {
     t128::wait_vmem();
     __syncthreads();
-    if (step + 1 < nsteps) issue(step + 1, (step + 1) & 1);
-    const int qrow0 = qstart + (step % ntq) * kKvBM;
+    nxt_q += kKvBM;
+    if (nxt_q >= a.Nq) {
+      nxt_q = qstart;
+      ++nxt_hq;
+    }
+    if (step + 1 < nsteps) issue(nxt_hq, nxt_q, (step + 1) & 1);
+    const int qrow0 = cur_q;
+    cur_q += kKvBM;
+    if (cur_q >= a.Nq) cur_q = qstart;
     const int64_t qp_first = a.q_pos0 + qrow0;
     const int64_t qp_last = qp_first + kKvBM - 1;
     if (kw0 >= a.Nk) continue;
