@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--c4-prefill", action="store_true",
+                    help="time the C4 model's per-layer attention share (GQA 32/8, 65,536 tokens, "
+                         "rank 3 of 4, forward) instead of the default workload")
     ap.add_argument("--long-shard", action="store_true",
                     help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
                          "against its diagonal block plus one full incoming 1M-token KV shard; "
@@ -187,6 +190,56 @@ def long_shard(args, torch, ra) -> int:
     return 0
 
 
+def c4_prefill(args, torch, ra) -> int:
+    """The C4 model's attention share on one GPU (prefill): GQA Hq=32 / Hkv=8,
+    d=128, bf16, 65,536 local tokens at rank 3 of a 4-rank ring, i.e. the
+    diagonal block plus 3 preceding 65,536-token KV shards, merged by LSE.
+    One step is one layer's attention; the model has 24 such layers."""
+    n, hq, hkv, d, world, rank = 65536, 32, 8, 128, 4, 3
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2468)
+    bf = torch.bfloat16
+    torch.cuda.reset_peak_memory_stats()
+    randn = lambda *s: torch.randn(*s, generator=gen, device=dev, dtype=torch.float32).to(bf)  # noqa: E731
+    log(f"C4 prefill attention: n={n} Hq={hq} Hkv={hkv} d={d} bf16, rank {rank} of {world}")
+    shards = [(randn(1, n, hq, d), randn(1, n, hkv, d), randn(1, n, hkv, d)) for _ in range(world)]
+
+    def step():
+        return ra.ring_causal_attention_forward_with_stats(shards, rank)
+
+    steps = max(1, min(args.steps, 3))
+    for _ in range(max(0, min(args.warmup, 1))):
+        step()
+    torch.cuda.synchronize()
+    log("C4 prefill attention: warmup done")
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    flops = (rank + 0.5) * 4.0 * n * n * hq * d
+    line = {
+        "metric": "C4 prefill attention TFLOP/s per layer (one GPU's share, GQA 32/8)",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": steps, "ms_per_step": round(ms, 2), "higher_is_better": True,
+        "pct_mfma_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "dtype": "bf16", "data": "synthetic: Q, K, V ~ N(0,1), seeded",
+        "config": {"workload": "C4 model attention share: 65,536 local tokens at rank 3 of 4, "
+                               "diagonal + 3 preceding KV shards, LSE merge; one layer",
+                   "local_tokens": n, "heads_q": hq, "heads_kv": hkv, "head_dim": d,
+                   "layers_in_model": 24},
+        "flops_per_step": flops,
+        "model_attention_ms_24_layers": round(24 * ms, 1),
+        "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -209,6 +262,8 @@ def main() -> int:
 
     if args.long_shard:
         return long_shard(args, torch, ra)
+    if args.c4_prefill:
+        return c4_prefill(args, torch, ra)
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")

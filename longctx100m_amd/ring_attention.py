@@ -237,34 +237,73 @@ def reference_causal_attention(q, k, v, causal: bool = True,
                                          precise=precise)
 
 
+def local_decode_backward(q, k, v, out, m, l, grad_out, *, causal: bool = True,
+                          q_position_start: int = 0, valid_length: Optional[int] = None,
+                          precise: bool = False):
+    """Single-rank backward with query positions from ``q_position_start`` and
+    key positions from 0 (_local_decode_backward,
+    src/longctx100m/ring_attention.py:258-287, taken by the autograd backward
+    when q_position_start is set and the group has one rank, :226-239).
+
+    The reference recomputes the probabilities with a dense softmax; here P
+    comes from the forward's (m, l), which hold the same row statistics for
+    the same positions.  delta uses ``out`` as given (the cast output, :314).
+    Returns (dq, dk, dv) in the dtypes of q, k, v."""
+    if q_position_start is None or q_position_start < 0:
+        raise ValueError("q_position_start must be a non-negative position")
+    _check_dev(q, k, v, out, grad_out)
+    b, n, hq, _ = q.shape
+    mm = m.reshape(b, hq, n).float().contiguous()
+    ll = l.reshape(b, hq, n).float().contiguous()
+    delta, lse2 = bwd_preprocess(out.contiguous(), grad_out.contiguous(), mm, ll)
+    dq = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+    dk = torch.zeros(k.shape, dtype=torch.float32, device=q.device)
+    dv = torch.zeros(k.shape, dtype=torch.float32, device=q.device)
+    bwd_shard(q, k, v, grad_out.contiguous(), lse2, delta, q_pos0=int(q_position_start),
+              k_pos0=0, causal=causal, valid_length=valid_length, dq_acc=dq, dk_acc=dk,
+              dv_acc=dv, precise=precise)
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
+
+
 class RingCausalAttention(torch.autograd.Function):
     """Autograd wrapper of one rank's share, mirroring _RingCausalAttention
     (src/longctx100m/ring_attention.py:194-255) with the in-process ring: the
     forward saves (out, m, l) and the backward recomputes P from them.
 
     Gradients flow to this rank's q, k and v; the other ranks' shards are
-    treated as constants (their owners differentiate their own shares)."""
+    treated as constants (their owners differentiate their own shares).
+    ``q_position_start`` applies to this rank's queries; with one rank the
+    backward takes the reference's decode path (local_decode_backward)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, shards, rank, causal, valid_length):
+    def forward(ctx, q, k, v, shards, rank, causal, valid_length, q_position_start=None):
         shards = list(shards)
         shards[rank] = (q.detach(), k.detach(), v.detach())
         outs, ms, ls = [], [], []
         for r in range(len(shards)):
+            qps = q_position_start if r == rank else None
             o, m, l = ring_causal_attention_forward_with_stats(shards, r, causal, 64, 128,
-                                                               valid_length)
+                                                               valid_length, qps)
             outs.append(o)
             ms.append(m)
             ls.append(l)
         ctx.shards, ctx.rank, ctx.causal, ctx.valid_length = shards, rank, causal, valid_length
+        ctx.q_position_start = q_position_start
         ctx.outs, ctx.ms, ctx.ls = outs, ms, ls
         return outs[rank]
 
     @staticmethod
     def backward(ctx, grad_out):
+        if ctx.q_position_start is not None and len(ctx.shards) == 1:
+            q, k, v = ctx.shards[0]
+            dq, dk, dv = local_decode_backward(
+                q, k, v, ctx.outs[0], ctx.ms[0], ctx.ls[0], grad_out.contiguous(),
+                causal=ctx.causal, q_position_start=ctx.q_position_start,
+                valid_length=ctx.valid_length)
+            return dq, dk, dv, None, None, None, None, None
         grad_outs = [torch.zeros_like(o) for o in ctx.outs]
         grad_outs[ctx.rank] = grad_out.contiguous()
         dq, dk, dv = ring_causal_attention_backward(ctx.shards, ctx.rank, ctx.outs, ctx.ms,
                                                     ctx.ls, grad_outs, ctx.causal, 64, 128,
-                                                    ctx.valid_length)
-        return dq, dk, dv, None, None, None, None
+                                                    ctx.valid_length, ctx.q_position_start)
+        return dq, dk, dv, None, None, None, None, None

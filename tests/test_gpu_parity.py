@@ -284,6 +284,25 @@ def test_ring_c2_shape_reduced(ra, gpu):
         assert norm_rel(_np(a), b) <= BF16_TOL
 
 
+def test_ring_c4_shape_reduced(ra, gpu):
+    """The C4 model's attention share (GQA Hq=32 / Hkv=8, d=128, bf16, the
+    local shard plus 3 preceding KV shards: rank 3 of a 4-rank ring) at 384
+    tokens per shard against the C restatement."""
+    rng = np.random.default_rng(4)
+    world, n, hq, hkv, d = 4, 384, 32, 8, 128
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, hq, hkv, d, gpu.bfloat16)
+    gos = [_t(gpu, rng.standard_normal((1, n, hq, d)), gpu.bfloat16) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    stats = [ra.ring_causal_attention_forward_with_stats(shards, r) for r in range(world)]
+    outs, ms, ls = (list(x) for x in zip(*stats))
+    fw, grads = _oracle_ring(qs, ks, vs, world, hq, hkv, rank=3, gos=gos)
+    assert norm_rel(_np(outs[3]), fw[3][0]) <= BF16_TOL
+    dq, dk, dv = ra.ring_causal_attention_backward(shards, 3, outs, ms, ls, gos)
+    gpu.cuda.synchronize()
+    for a, b in zip((dq, dk, dv), grads):
+        assert norm_rel(_np(a), b) <= BF16_TOL
+
+
 def test_host_pointer_entry_points(gpu):
     """lc_ring_fwd_with_stats_host / lc_ring_bwd_host (the CPU-tensor form a
     candle backend binds) agree with the oracle."""
@@ -350,6 +369,41 @@ def test_autograd_wrapper(ra, gpu):
     assert norm_rel(_np(q.grad), edq) <= BF16_TOL
     assert norm_rel(_np(k.grad), edk[:, n:]) <= BF16_TOL
     assert norm_rel(_np(v.grad), edv[:, n:]) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype_name,d,valid_length,qps", [
+    ("bfloat16", 128, None, 57),
+    ("bfloat16", 64, 150, 300),
+    ("float32", 128, 170, 0),
+    ("float32", 96, None, 13),
+])
+def test_decode_path_q_position_start(ra, gpu, dtype_name, d, valid_length, qps):
+    """One rank with q_position_start: the forward places queries at
+    qps + i and keys at j (ring_attention.py:117-130 with world 1) and the
+    autograd backward takes _local_decode_backward (py:226-239, :258-287).
+    Checked against the fp64 dense closed form at the same positions."""
+    import torch
+
+    dtype = getattr(gpu, dtype_name)
+    rng = np.random.default_rng(zlib.crc32(repr((dtype_name, d, valid_length, qps)).encode()))
+    n, hq, hkv = 200, 4, 2
+    qs, ks, vs = _rand_shards(gpu, rng, 1, n, hq, hkv, d, dtype)
+    q = qs[0].clone().requires_grad_()
+    k = ks[0].clone().requires_grad_()
+    v = vs[0].clone().requires_grad_()
+    out = ra.RingCausalAttention.apply(q, k, v, [(q, k, v)], 0, True, valid_length, qps)
+    go = _t(gpu, rng.standard_normal((1, n, hq, d)), dtype)
+    out.backward(go)
+    tol = BF16_TOL if dtype_name == "bfloat16" else FP32_TOL
+    eo = dense.attention_fwd(_np(qs[0]), _np(ks[0]), _np(vs[0]), q_pos0=qps, k_pos0=0,
+                             valid_length=valid_length)[0]
+    assert norm_rel(_np(out), eo) <= tol
+    oref = _np(out) if dtype_name == "bfloat16" else eo  # delta uses the cast output
+    edq, edk, edv = dense.attention_bwd(_np(qs[0]), _np(ks[0]), _np(vs[0]), _np(go), q_pos0=qps,
+                                        k_pos0=0, valid_length=valid_length, out=oref)
+    assert norm_rel(_np(q.grad), edq) <= tol
+    assert norm_rel(_np(k.grad), edk) <= tol
+    assert norm_rel(_np(v.grad), edv) <= tol
 
 
 def test_full_size_c2_c3_spot_check(ra, gpu):
