@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--c4-prefill", action="store_true",
                     help="time the C4 model's per-layer attention share (GQA 32/8, 65,536 tokens, "
                          "rank 3 of 4, forward) instead of the default workload")
+    ap.add_argument("--c4-model", action="store_true",
+                    help="time the whole C4 model prefill share (embedding, 24 layers, LM head)")
     ap.add_argument("--long-shard", action="store_true",
                     help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
                          "against its diagonal block plus one full incoming 1M-token KV shard; "
@@ -240,6 +242,92 @@ def c4_prefill(args, torch, ra) -> int:
     return 0
 
 
+def c4_model(args, torch, ra) -> int:
+    """the C4 model's prefill on one GPU's share.  Token ids
+    of a 65,536-token local shard -> embedding -> 24 decoder layers (RMSNorm,
+    fused QKV GEMM, RoPE, ring attention at rank 3 of 4 over the diagonal block
+    and 3 preceding KV shards, O GEMM, RMSNorm, fused gate/up GEMM, SwiGLU,
+    down GEMM; residual adds fused into the norms) -> final RMSNorm -> LM head.
+    Random-init bf16 weights N(0, 0.02); the preceding ranks' K/V shards are
+    seeded random tensors per layer."""
+    from longctx100m_amd import layer as ly
+
+    cfg = ly.C4
+    n, rank, world, d = 65536, 3, 4, cfg.head_dim
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1357)
+    bf = torch.bfloat16
+    torch.cuda.reset_peak_memory_stats()
+    log(f"C4 model prefill: {cfg.num_layers} layers, hidden {cfg.hidden_size}, "
+        f"GQA {cfg.num_heads}/{cfg.num_key_value_heads}, {n} tokens at rank {rank} of {world}")
+    randn = lambda *s: (torch.randn(*s, generator=gen, device=dev, dtype=torch.float32) * 0.02).to(bf)  # noqa: E731
+    embed = randn(cfg.vocab_size, cfg.hidden_size)
+    lm_head = randn(cfg.vocab_size, cfg.hidden_size)
+    final_norm = torch.ones(cfg.hidden_size, device=dev, dtype=bf)
+    layers = [ly.init_layer_weights(cfg, gen, dev) for _ in range(cfg.num_layers)]
+    kv = [[(torch.randn(1, n, cfg.num_key_value_heads, d, generator=gen, device=dev).to(bf),
+            torch.randn(1, n, cfg.num_key_value_heads, d, generator=gen, device=dev).to(bf))
+           for _ in range(rank)] for _ in range(cfg.num_layers)]
+    ids = torch.randint(0, cfg.vocab_size, (n,), generator=gen, device=dev)
+    table = ly.rope_table(ly.rope_params(d, cfg.rope_theta, cfg.rope_scaling), n, rank * n)
+    log("C4 model prefill: weights and inputs ready")
+
+    def prefill(timers=None):
+        x = torch.nn.functional.embedding(ids, embed)
+        res = None
+        for li in range(cfg.num_layers):
+            x, res = ly.layer_prefill(x, layers[li], cfg, table, rank, kv[li], residual=res,
+                                      timers=timers if li == 0 else None)
+        h = ly.rmsnorm(x, final_norm, cfg.rms_norm_eps, residual=res)
+        return torch.matmul(h, lm_head.t())
+
+    for _ in range(max(0, min(args.warmup, 1))):
+        prefill()
+    torch.cuda.synchronize()
+    log("C4 model prefill: warmup done")
+    timers = {}
+    steps = max(1, min(args.steps, 2))
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        logits = prefill(timers)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    # per-category time of the first layer (last timed step)
+    ev = timers.get("_events", [])[-13:]
+    cat = {}
+    for (_, a), (name, b) in zip(ev, ev[1:]):
+        cat[name] = cat.get(name, 0.0) + a.elapsed_time(b)
+    fl = ly.layer_flops(cfg, n, rank)
+    head = 2.0 * n * cfg.hidden_size * cfg.vocab_size
+    flops = cfg.num_layers * (fl["gemm"] + fl["attention"]) + head
+    line = {
+        "metric": "C4 model prefill TFLOP/s (one GPU's share: 65,536 tokens at rank 3 of 4)",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": steps, "ms_per_step": round(ms, 1), "higher_is_better": True,
+        "pct_mfma_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "tokens_per_s": round(n / (ms * 1e-3), 1),
+        "dtype": "bf16",
+        "data": "synthetic: token ids uniform over the vocab, weights N(0,0.02), preceding KV "
+                "shards N(0,1), seeded",
+        "config": {"workload": "BASELINE config 4: 24-layer Llama-style prefill share, hidden 4096, "
+                               "Hq=32, Hkv=8, d=128, SwiGLU 14336, vocab 128256, 65,536 local "
+                               "tokens + 3 preceding KV shards per layer",
+                   "local_tokens": n, "layers": cfg.num_layers},
+        "flops_per_step": flops,
+        "flops_split": {"attention": cfg.num_layers * fl["attention"],
+                        "gemm": cfg.num_layers * fl["gemm"] + head},
+        "layer0_ms": {k: round(v, 3) for k, v in cat.items()},
+        "logits_shape": list(logits.shape),
+        "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -264,6 +352,8 @@ def main() -> int:
         return long_shard(args, torch, ra)
     if args.c4_prefill:
         return c4_prefill(args, torch, ra)
+    if args.c4_model:
+        return c4_model(args, torch, ra)
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")

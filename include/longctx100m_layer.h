@@ -1,0 +1,85 @@
+/*
+ * longctx100m_layer -- MI355X (gfx950) kernels around the attention of one
+ * decoder layer's prefill share: RMSNorm (with the residual add fused), RoPE
+ * and the SwiGLU gate.  Same library and conventions as longctx100m_attn.h
+ * (device pointers, a hipStream_t passed as void*, LC_* status codes,
+ * lc_last_error()).  The GEMMs of the layer are plain library GEMMs
+ * (hipBLASLt through the caller) and are not part of this ABI.
+ *
+ * Tensors are row-major.  A "row" is one token: x [rows, cols] for RMSNorm and
+ * SwiGLU, [tokens, heads, head_dim] for RoPE (batch folded into tokens: every
+ * row of a batch shares the position table of its token index).
+ * Arithmetic is fp32; bf16 results are rounded to nearest even at the same
+ * points the reference rounds (noted per entry).
+ */
+#ifndef LONGCTX100M_LAYER_H
+#define LONGCTX100M_LAYER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "longctx100m_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* RMSNorm, replacing RmsNorm::forward (rust/longctx100m-model/src/model.rs:53-62;
+ * src/longctx100m/model.py:114-118):
+ *   h   = x (+ residual, rounded to dtype, when residual != NULL)
+ *   out = dtype(dtype(h * 1/sqrt(mean(h^2) + eps)) * weight)
+ * h is written to residual_out when that pointer is non-NULL: the decoder's
+ * residual stream x + attn(x), model.rs:387-393, computed once.  x, residual,
+ * residual_out and out are [rows, cols] with row strides in elements; weight
+ * is [cols].  cols must be a multiple of 8 and <= 16384. */
+int lc_rmsnorm(int32_t dtype, int64_t rows, int32_t cols, float eps, const void* x,
+               int64_t x_stride, const void* residual, int64_t residual_stride,
+               void* residual_out, const void* weight, void* out, int64_t out_stride,
+               void* stream);
+
+/* RoPE scaling profile (rust/longctx100m-model/src/rope.rs:15-99; config
+ * rope_scaling).  type: 0 default, 1 linear, 2 llama3. */
+typedef struct lc_rope {
+  int32_t head_dim; /* even, <= 256 */
+  int32_t type;
+  double theta;
+  double factor;                           /* linear, llama3 */
+  double low_freq_factor;                  /* llama3 */
+  double high_freq_factor;                 /* llama3 */
+  double original_max_position_embeddings; /* llama3 */
+  double attention_factor;                 /* llama3 (scales cos only, rope.rs:109-114) */
+} lc_rope_t;
+
+/* Inverse frequencies of rope.rs:15-99 on the host (fp32, head_dim / 2 values)
+ * and the cosine factor; validation messages are rope.rs's texts. */
+int lc_rope_inv_freq(const lc_rope_t* rope, float* inv_freq, float* cos_factor);
+
+/* Position table for tokens pos0 .. pos0 + tokens - 1 (rope.rs:101-114):
+ * table [tokens, 2, head_dim / 2] fp32 holding cos(f) * cos_factor and sin(f)
+ * with f = position * inv_freq (position scaled by 1/factor for the linear
+ * profile). */
+int lc_rope_table(const lc_rope_t* rope, int64_t tokens, int64_t pos0, float* table,
+                  void* stream);
+
+/* Rotate-half RoPE (rope.rs:116-127): for each [token, head] row of src,
+ *   dst[:h] = x1 * cos - x2 * sin,  dst[h:] = x2 * cos + x1 * sin   (h = head_dim / 2)
+ * in fp32, rounded to dtype.  src rows may be strided (e.g. the q or k columns
+ * of a fused QKV projection: src_token_stride elements between tokens, heads
+ * contiguous); dst is contiguous [tokens, heads, head_dim].  dst may equal src
+ * when src is contiguous. */
+int lc_rope_apply(int32_t dtype, int64_t tokens, int32_t heads, int32_t head_dim,
+                  const float* table, const void* src, int64_t src_token_stride, void* dst,
+                  void* stream);
+
+/* SwiGLU gate (model.rs:323-327; src/longctx100m/model.py SwiGLU):
+ *   out = dtype(dtype(silu(gate)) * up),  silu(g) = g / (1 + exp(-g)) in fp32.  gate and up are [rows, cols] with row
+ * strides (e.g. the two halves of one fused gate/up projection); out is
+ * contiguous [rows, cols].  cols must be a multiple of 8. */
+int lc_swiglu(int32_t dtype, int64_t rows, int32_t cols, const void* gate, int64_t gate_stride,
+              const void* up, int64_t up_stride, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LONGCTX100M_LAYER_H */

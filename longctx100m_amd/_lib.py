@@ -1,4 +1,5 @@
-"""ctypes binding of liblongctx100m_attn.so (include/longctx100m_attn.h).
+"""ctypes binding of liblongctx100m_attn.so (include/longctx100m_attn.h and
+include/longctx100m_layer.h).
 
 Loading never falls back to anything: if the library is missing the import
 of the product path fails with a message naming the build command.
@@ -65,6 +66,19 @@ class RingDesc(ctypes.Structure):
     ]
 
 
+class Rope(ctypes.Structure):
+    _fields_ = [
+        ("head_dim", c_int32),
+        ("type", c_int32),
+        ("theta", ctypes.c_double),
+        ("factor", ctypes.c_double),
+        ("low_freq_factor", ctypes.c_double),
+        ("high_freq_factor", ctypes.c_double),
+        ("original_max_position_embeddings", ctypes.c_double),
+        ("attention_factor", ctypes.c_double),
+    ]
+
+
 _vpp = POINTER(c_void_p)
 _S, _M, _R = POINTER(Shape), POINTER(Mask), POINTER(RingDesc)
 
@@ -93,6 +107,14 @@ SIGNATURES = {
     "lc_reference_causal_attention_host": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32,
                                                    c_int32, c_void_p, c_void_p, c_void_p,
                                                    c_int32, c_int64, c_void_p]),
+    "lc_rmsnorm": (c_int, [c_int32, c_int64, c_int32, ctypes.c_float, c_void_p, c_int64, c_void_p,
+                           c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "lc_rope_inv_freq": (c_int, [POINTER(Rope), c_void_p, c_void_p]),
+    "lc_rope_table": (c_int, [POINTER(Rope), c_int64, c_int64, c_void_p, c_void_p]),
+    "lc_rope_apply": (c_int, [c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_int64,
+                              c_void_p, c_void_p]),
+    "lc_swiglu": (c_int, [c_int32, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_int64,
+                          c_void_p, c_void_p]),
     "lc_last_error": (ctypes.c_char_p, []),
     "lc_abi_version": (c_int32, []),
 }

@@ -37,6 +37,13 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source extras.  layer.hip restates the reference's separately rounded
+# tensor ops, so nothing in it may be contracted into fused multiply-adds.
+EXTRA_FLAGS = {
+    "layer.hip": ["-ffp-contract=off"],
+}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -46,7 +53,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

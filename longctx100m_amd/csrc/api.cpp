@@ -21,8 +21,10 @@
 #include "kernels.h"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace lc {
 
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
@@ -37,6 +39,13 @@ int set_error(int code, const char* fmt, ...) {
 int hip_error(hipError_t e, const char* where) {
   return set_error(LC_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
 }
+
+}  // namespace lc
+
+namespace {
+
+using lc::hip_error;
+using lc::set_error;
 
 #define LC_TRY_HIP(expr, where)                \
   do {                                         \

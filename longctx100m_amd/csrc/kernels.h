@@ -74,4 +74,22 @@ hipError_t launch_bwd_preprocess(int B, int N, int H, int D, int dtype, const vo
                                  const void* dout, const float* m, const float* l, float* delta,
                                  float* lse2, hipStream_t s);
 
+// Decoder-layer row kernels (layer.hip).
+hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
+                          int64_t xs, const void* res, int64_t rs, void* res_out, const void* w,
+                          void* out, int64_t os, hipStream_t s);
+hipError_t launch_rope_table(const float* inv, int half, float cos_factor, bool linear,
+                             float pos_scale, int64_t tokens, int64_t pos0, float* table,
+                             hipStream_t s);
+hipError_t launch_rope_apply(int dtype, int64_t tokens, int heads, int head_dim,
+                             const float* table, const void* src, int64_t sts, void* dst,
+                             hipStream_t s);
+hipError_t launch_swiglu(int dtype, int64_t rows, int cols, const void* g, int64_t gs,
+                         const void* u, int64_t us, void* out, hipStream_t s);
+
+// Error reporting shared by the C-ABI translation units: set the calling
+// thread's lc_last_error() text and return the code.
+int set_error(int code, const char* fmt, ...);
+int hip_error(hipError_t e, const char* where);
+
 }  // namespace lc

@@ -1,0 +1,287 @@
+// Row kernels around one decoder layer's attention (gfx950): RMSNorm with the
+// residual add fused, the RoPE position table and rotate-half RoPE, and the
+// SwiGLU gate.  All are HBM-bound streams: 16-byte vector loads and stores,
+// fp32 arithmetic, bf16 rounding at the points the reference rounds.
+//
+//   RMSNorm  rust/longctx100m-model/src/model.rs:53-62 (decoder use :387-393)
+//   RoPE     rust/longctx100m-model/src/rope.rs:101-127
+//   SwiGLU   rust/longctx100m-model/src/model.rs:323-327
+#include "common.h"
+#include "kernels.h"
+
+// Each product and sum rounds on its own, as the reference's tensor ops do:
+// no contraction into fused multiply-adds in this file (the build also passes
+// -ffp-contract=off for it; sums of squares use an explicit fmaf).
+#pragma clang fp contract(off)
+
+namespace lc {
+namespace {
+
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// 8 consecutive elements as fp32 (one 16-byte load for bf16, two for fp32).
+template <typename T>
+__device__ __forceinline__ f32x8 load8(const T* p);
+template <>
+__device__ __forceinline__ f32x8 load8<uint16_t>(const uint16_t* p) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  f32x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[2 * i] = __uint_as_float(w[i] << 16);
+    r[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+  return r;
+}
+template <>
+__device__ __forceinline__ f32x8 load8<float>(const float* p) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  return f32x8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const f32x8& v);
+template <>
+__device__ __forceinline__ void store8<uint16_t>(uint16_t* p, const f32x8& v) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+  *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const f32x8& v) {
+  *reinterpret_cast<float4*>(p) = float4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<float4*>(p + 4) = float4{v[4], v[5], v[6], v[7]};
+}
+
+// Round to the storage type and back (identity for fp32).
+template <typename T>
+__device__ __forceinline__ float rnd(float x);
+template <>
+__device__ __forceinline__ float rnd<float>(float x) {
+  return x;
+}
+template <>
+__device__ __forceinline__ float rnd<uint16_t>(float x) {
+  return bf16_to_f32(f32_to_bf16(x));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// ---------------------------------------------------------------- RMSNorm --
+// One wave per row; each lane keeps its 8-element chunks of the row in
+// registers between the sum of squares and the scaling.
+constexpr int kNormMaxChunks = 32;  // cols <= 64 * 8 * 32 = 16384
+
+template <typename T, int NC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, float eps,
+                                                      const T* x, int64_t xs, const T* res,
+                                                      int64_t rs, T* res_out, const T* w,
+                                                      T* out, int64_t os) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nchunk = cols / 8;
+  f32x8 v[NC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunk) {
+      f32x8 h = load8<T>(x + row * xs + 8 * c);
+      if (res != nullptr) {
+        const f32x8 r = load8<T>(res + row * rs + 8 * c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = rnd<T>(h[j] + r[j]);  // x + attn(x) in the model dtype
+        if (res_out != nullptr) store8<T>(res_out + row * xs + 8 * c, h);
+      }
+      v[i] = h;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  // mean(h^2) + eps, then sqrt and reciprocal as two rounded steps (model.rs:57).
+  const float inv = 1.0f / __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), eps));
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunk) {
+      const f32x8 wt = load8<T>(w + 8 * c);
+      f32x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = rnd<T>(rnd<T>(__fmul_rn(v[i][j], inv)) * wt[j]);
+      store8<T>(out + row * os + 8 * c, o);
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_rmsnorm_t(int64_t rows, int cols, float eps, const void* x, int64_t xs,
+                            const void* res, int64_t rs, void* res_out, const void* w, void* out,
+                            int64_t os, hipStream_t s) {
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  const int nchunk = cols / 8;
+  auto args = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, rows, cols, eps, static_cast<const T*>(x), xs,
+                       static_cast<const T*>(res), rs, static_cast<T*>(res_out),
+                       static_cast<const T*>(w), static_cast<T*>(out), os);
+  };
+  if (nchunk <= 64 * 2)
+    args(rmsnorm_kernel<T, 2>);
+  else if (nchunk <= 64 * 8)
+    args(rmsnorm_kernel<T, 8>);
+  else
+    args(rmsnorm_kernel<T, kNormMaxChunks>);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------- RoPE --
+struct RopeTableArgs {
+  float inv[128];
+  float cos_factor;
+  float pos_scale;  // 1/factor for the linear profile
+  int linear;
+  int half;
+  int64_t tokens, pos0;
+  float* table;
+};
+
+// table[t][0][i] = cos(f) * cos_factor, table[t][1][i] = sin(f), f = pos * inv[i]
+// with the position converted to fp32 first (rope.rs:101-114).
+__global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.tokens * a.half) return;
+  const int64_t t = idx / a.half;
+  const int i = (int)(idx - t * a.half);
+  float pos = (float)(a.pos0 + t);
+  if (a.linear) pos = __fmul_rn(pos, a.pos_scale);
+  const float f = __fmul_rn(pos, a.inv[i]);
+  float* row = a.table + t * 2 * a.half;
+  row[i] = __fmul_rn(cosf(f), a.cos_factor);
+  row[a.half + i] = sinf(f);
+}
+
+// One thread per (token, head, 8 rotation pairs): x1 = x[8c..8c+7] and
+// x2 = x[half+8c..], out1 = x1*cos - x2*sin, out2 = x2*cos + x1*sin.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_apply_kernel(int64_t tokens, int heads, int half,
+                                                         const float* table, const T* src,
+                                                         int64_t sts, T* dst) {
+  const int cph = half / 8;  // chunks per head
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = tokens * heads * cph;
+  if (idx >= total) return;
+  const int c = (int)(idx % cph);
+  const int64_t th = idx / cph;
+  const int h = (int)(th % heads);
+  const int64_t t = th / heads;
+  const T* s = src + t * sts + (int64_t)h * 2 * half + 8 * c;
+  T* d = dst + (t * heads + h) * 2 * half + 8 * c;
+  const f32x8 x1 = load8<T>(s);
+  const f32x8 x2 = load8<T>(s + half);
+  const float* tr = table + t * 2 * half + 8 * c;
+  const f32x8 cs = load8<float>(tr);
+  const f32x8 sn = load8<float>(tr + half);
+  f32x8 o1, o2;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    o1[j] = x1[j] * cs[j] - x2[j] * sn[j];
+    o2[j] = x2[j] * cs[j] + x1[j] * sn[j];
+  }
+  store8<T>(d, o1);
+  store8<T>(d + half, o2);
+}
+
+// ----------------------------------------------------------------- SwiGLU --
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(int64_t rows, int cols, const T* g,
+                                                     int64_t gs, const T* u, int64_t us,
+                                                     T* out) {
+  const int cpr = cols / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * cpr) return;
+  const int64_t r = idx / cpr;
+  const int c = (int)(idx - r * cpr);
+  const f32x8 gv = load8<T>(g + r * gs + 8 * c);
+  const f32x8 uv = load8<T>(u + r * us + 8 * c);
+  f32x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sl = rnd<T>(__fdiv_rn(gv[j], __fadd_rn(1.0f, expf(-gv[j]))));
+    o[j] = __fmul_rn(sl, uv[j]);
+  }
+  store8<T>(out + r * (int64_t)cols + 8 * c, o);
+}
+
+unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
+                          int64_t xs, const void* res, int64_t rs, void* res_out, const void* w,
+                          void* out, int64_t os, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  return dtype == 1 ? launch_rmsnorm_t<uint16_t>(rows, cols, eps, x, xs, res, rs, res_out, w, out,
+                                                 os, s)
+                    : launch_rmsnorm_t<float>(rows, cols, eps, x, xs, res, rs, res_out, w, out,
+                                              os, s);
+}
+
+hipError_t launch_rope_table(const float* inv, int half, float cos_factor, bool linear,
+                             float pos_scale, int64_t tokens, int64_t pos0, float* table,
+                             hipStream_t s) {
+  if (tokens <= 0) return hipSuccess;
+  RopeTableArgs a;
+  for (int i = 0; i < half; ++i) a.inv[i] = inv[i];
+  a.cos_factor = cos_factor;
+  a.pos_scale = pos_scale;
+  a.linear = linear ? 1 : 0;
+  a.half = half;
+  a.tokens = tokens;
+  a.pos0 = pos0;
+  a.table = table;
+  hipLaunchKernelGGL(rope_table_kernel, dim3(blocks_for(tokens * half)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_apply(int dtype, int64_t tokens, int heads, int head_dim,
+                             const float* table, const void* src, int64_t sts, void* dst,
+                             hipStream_t s) {
+  const int half = head_dim / 2;
+  const int64_t n = tokens * heads * (half / 8);
+  if (n <= 0) return hipSuccess;
+  if (dtype == 1)
+    hipLaunchKernelGGL(rope_apply_kernel<uint16_t>, dim3(blocks_for(n)), dim3(256), 0, s, tokens,
+                       heads, half, table, static_cast<const uint16_t*>(src), sts,
+                       static_cast<uint16_t*>(dst));
+  else
+    hipLaunchKernelGGL(rope_apply_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, tokens,
+                       heads, half, table, static_cast<const float*>(src), sts,
+                       static_cast<float*>(dst));
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(int dtype, int64_t rows, int cols, const void* g, int64_t gs,
+                         const void* u, int64_t us, void* out, hipStream_t s) {
+  const int64_t n = rows * (cols / 8);
+  if (n <= 0) return hipSuccess;
+  if (dtype == 1)
+    hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3(blocks_for(n)), dim3(256), 0, s, rows, cols,
+                       static_cast<const uint16_t*>(g), gs, static_cast<const uint16_t*>(u), us,
+                       static_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, rows, cols,
+                       static_cast<const float*>(g), gs, static_cast<const float*>(u), us,
+                       static_cast<float*>(out));
+  return hipGetLastError();
+}
+
+}  // namespace lc

@@ -1,0 +1,233 @@
+"""Decoder-layer prefill share on MI355X: RMSNorm, RoPE and SwiGLU kernels
+(include/longctx100m_layer.h) around the ring attention of this package, with
+the projections as library GEMMs (torch.matmul -> hipBLASLt).
+
+Mirrors the reference's decoder (rust/longctx100m-model/src/model.rs:387-393):
+    h = RMSNorm(x); q, k, v = proj(h); q, k = RoPE(q, k); a = attention(q, k, v)
+    x = x + o_proj(a); h = RMSNorm(x); x = x + down(silu(gate(h)) * up(h))
+with the attention of one rank's shard taken over the ring
+(SelfAttention::forward_ring, model.rs:155-222).  The q/k/v projections run
+as one GEMM against the stacked [q; k; v] weight, and gate/up as one GEMM
+against [gate; up].  RoPE writes the q and k columns of the fused output
+straight into contiguous attention inputs, and each residual add is fused
+into the RMSNorm that follows it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from . import ring_attention as ra
+from .ring_attention import _dtype_code, _stream
+
+
+def _chk_cuda(*ts):
+    for t in ts:
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError("tensors must live on the GPU (device pointers are passed to HIP)")
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: Optional[torch.Tensor] = None, residual_out: Optional[torch.Tensor] = None,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm over the last dim (model.rs:53-62); with ``residual`` the input
+    is x + residual (rounded to the dtype), written to ``residual_out`` if given."""
+    _chk_cuda(x, weight)
+    cols = x.shape[-1]
+    x2 = x.reshape(-1, cols)
+    if x2.stride(-1) != 1:
+        raise ValueError("rows must be contiguous")
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device) if out is None else out
+    r2 = residual.reshape(-1, cols) if residual is not None else None
+    ro = residual_out.reshape(-1, cols) if residual_out is not None else None
+    if ro is not None and ro.stride(0) != x2.stride(0):
+        raise ValueError("residual_out must share x's row stride")
+    _lib.check(_lib.load().lc_rmsnorm(
+        _dtype_code(x), x2.shape[0], cols, float(eps), x2.data_ptr(), x2.stride(0),
+        r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
+        ro.data_ptr() if ro is not None else None, weight.data_ptr(), out.data_ptr(),
+        out.reshape(-1, cols).stride(0), _stream()))
+    return out.reshape(x.shape)
+
+
+def rope_params(head_dim: int, theta: float, rope_scaling: Optional[dict] = None) -> _lib.Rope:
+    """The lc_rope_t of a config's rope_theta / rope_scaling (rope.rs:24-99)."""
+    r = _lib.Rope(head_dim, 0, float(theta), 1.0, 0.0, 0.0, 0.0, 1.0)
+    if rope_scaling:
+        kind = rope_scaling.get("rope_type", rope_scaling.get("type", "default"))
+        r.type = {"default": 0, "linear": 1, "llama3": 2}.get(kind, -1)
+        if r.type < 0:
+            raise ValueError(f"unsupported RoPE type {kind!r}")
+        r.factor = float(rope_scaling.get("factor", 1.0))
+        if r.type == 2:
+            need = ("low_freq_factor", "high_freq_factor", "original_max_position_embeddings")
+            if any(k not in rope_scaling for k in need):
+                raise ValueError("llama3 RoPE needs low/high frequency factors and original "
+                                 "context length")
+            r.low_freq_factor = float(rope_scaling["low_freq_factor"])
+            r.high_freq_factor = float(rope_scaling["high_freq_factor"])
+            r.original_max_position_embeddings = float(
+                rope_scaling["original_max_position_embeddings"])
+            r.attention_factor = float(rope_scaling.get("attention_factor", 1.0))
+    return r
+
+
+def rope_inv_freq(rope: _lib.Rope) -> Tuple[List[float], float]:
+    """Host inverse frequencies and cosine factor (no GPU needed)."""
+    inv = (ctypes.c_float * (rope.head_dim // 2))()
+    cf = ctypes.c_float()
+    _lib.check(_lib.load().lc_rope_inv_freq(ctypes.byref(rope), ctypes.addressof(inv),
+                                            ctypes.addressof(cf)))
+    return list(inv), cf.value
+
+
+def rope_table(rope: _lib.Rope, tokens: int, pos0: int, device="cuda") -> torch.Tensor:
+    """[tokens, 2, head_dim/2] fp32 cos/sin table for positions pos0 .. pos0+tokens-1."""
+    table = torch.empty((tokens, 2, rope.head_dim // 2), dtype=torch.float32, device=device)
+    _lib.check(_lib.load().lc_rope_table(ctypes.byref(rope), tokens, pos0, table.data_ptr(),
+                                         _stream()))
+    return table
+
+
+def rope_apply(src: torch.Tensor, table: torch.Tensor, heads: int, head_dim: int,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotate-half RoPE of the [tokens, heads*head_dim] columns ``src`` (row stride
+    free, e.g. a column slice of the fused QKV output) into contiguous
+    [tokens, heads, head_dim] (rope.rs:116-127)."""
+    _chk_cuda(src, table)
+    tokens = src.shape[0]
+    if src.dim() != 2 or src.shape[1] != heads * head_dim or src.stride(1) != 1:
+        raise ValueError("src must be [tokens, heads*head_dim] with contiguous rows")
+    out = torch.empty((tokens, heads, head_dim), dtype=src.dtype, device=src.device) \
+        if out is None else out
+    _lib.check(_lib.load().lc_rope_apply(_dtype_code(src), tokens, heads, head_dim,
+                                         table.data_ptr(), src.data_ptr(), src.stride(0),
+                                         out.data_ptr(), _stream()))
+    return out
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None):
+    """silu(gate) * up over [rows, cols] views (row strides free)."""
+    _chk_cuda(gate, up)
+    rows, cols = gate.shape
+    if up.shape != gate.shape or gate.stride(1) != 1 or up.stride(1) != 1:
+        raise ValueError("gate and up must be [rows, cols] with contiguous rows")
+    out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device) if out is None else out
+    _lib.check(_lib.load().lc_swiglu(_dtype_code(gate), rows, cols, gate.data_ptr(),
+                                     gate.stride(0), up.data_ptr(), up.stride(0),
+                                     out.data_ptr(), _stream()))
+    return out
+
+
+# ------------------------------------------------------------- the model --
+
+@dataclass
+class ModelConfig:
+    """The fields of rust/longctx100m-model/src/config.rs this path uses."""
+    hidden_size: int = 4096
+    num_heads: int = 32
+    num_key_value_heads: int = 8
+    intermediate_size: int = 14336
+    num_layers: int = 24
+    vocab_size: int = 128256
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    rope_scaling: Optional[dict] = None
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+
+C4 = ModelConfig()
+
+
+def init_layer_weights(cfg: ModelConfig, gen: torch.Generator, device, dtype=torch.bfloat16,
+                       std: float = 0.02) -> Dict[str, torch.Tensor]:
+    """Random-init weights of one decoder layer: N(0, std) projections, unit
+    RMSNorm weights (RmsNorm::new's Init::Const(1.0), model.rs:43-46)."""
+    d, hq, hkv = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    c, inter = cfg.hidden_size, cfg.intermediate_size
+
+    def randn(*shape):
+        return (torch.randn(*shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+    return {
+        "wqkv": randn((hq + 2 * hkv) * d, c),  # rows: q_proj, k_proj, v_proj
+        "wo": randn(c, hq * d),
+        "wgu": randn(2 * inter, c),            # rows: gate_proj, up_proj
+        "wd": randn(c, inter),
+        "norm1": torch.ones(c, device=device, dtype=dtype),
+        "norm2": torch.ones(c, device=device, dtype=dtype),
+    }
+
+
+def layer_prefill(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
+                  table: torch.Tensor, rank: int,
+                  preceding_kv: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                  residual: Optional[torch.Tensor] = None,
+                  timers: Optional[Dict[str, list]] = None):
+    """One decoder layer over this rank's shard x [T, hidden].
+
+    ``preceding_kv`` holds the (k, v) [1, T, Hkv, d] shards of ranks 0..rank-1
+    (the ring's incoming KV).  ``residual``, when given, is the previous
+    layer's MLP output still to be added to x (the add is fused into this
+    layer's first RMSNorm).  Returns (x_after_attention, mlp_out): the layer
+    output is their sum, which the next layer's (or the final) RMSNorm forms."""
+    T, c = x.shape
+    d, hq, hkv = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    if len(preceding_kv) != rank:
+        raise ValueError("preceding_kv must hold one (k, v) per earlier rank")
+
+    def tick(name):
+        if timers is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            timers.setdefault("_events", []).append((name, e))
+
+    tick("start")
+    if residual is not None:
+        xin = torch.empty_like(x)
+        h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps, residual=residual, residual_out=xin)
+    else:
+        xin = x
+        h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps)
+    tick("norm")
+    qkv = torch.matmul(h, w["wqkv"].t())
+    tick("gemm")
+    q = rope_apply(qkv[:, :hq * d], table, hq, d)
+    k = rope_apply(qkv[:, hq * d:(hq + hkv) * d], table, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].contiguous().view(T, hkv, d)
+    tick("rope")
+    qb, kb, vb = q.view(1, T, hq, d), k.view(1, T, hkv, d), v.view(1, T, hkv, d)
+    shards = [(qb, pk, pv) for pk, pv in preceding_kv] + [(qb, kb, vb)]
+    attn, _, _ = ra.ring_causal_attention_forward_with_stats(shards, rank)
+    tick("attention")
+    o = torch.matmul(attn.view(T, hq * d), w["wo"].t())
+    tick("gemm")
+    x2 = torch.empty_like(x)
+    h2 = rmsnorm(xin, w["norm2"], cfg.rms_norm_eps, residual=o, residual_out=x2)
+    tick("norm")
+    gu = torch.matmul(h2, w["wgu"].t())
+    tick("gemm")
+    inter = cfg.intermediate_size
+    a = swiglu(gu[:, :inter], gu[:, inter:])
+    tick("swiglu")
+    mlp = torch.matmul(a, w["wd"].t())
+    tick("gemm")
+    return x2, mlp
+
+
+def layer_flops(cfg: ModelConfig, tokens: int, rank: int) -> Dict[str, float]:
+    """Algorithmic FLOPs of one layer's prefill share: GEMMs and attention
+    (4*Nq*Nk*Hq*d per full shard pair, the diagonal counting half)."""
+    d, hq, hkv = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    c, inter = cfg.hidden_size, cfg.intermediate_size
+    gemm = 2.0 * tokens * c * ((hq + 2 * hkv) * d + hq * d + 2 * inter) + 2.0 * tokens * inter * c
+    attn = (rank + 0.5) * 4.0 * tokens * tokens * hq * d
+    return {"gemm": gemm, "attention": attn}

@@ -14,6 +14,8 @@ Two independent oracles live here:
   a rank's ring output equals its rows of dense causal attention over the
   concatenated sequence (tests/test_ring_attention.py:300 and
   ring_attention.rs:548-561 in the reference).
+* ``layer`` -- numpy float32 restatements of the decoder-layer row ops around
+  attention (RMSNorm, RoPE, SwiGLU; model.rs and rope.rs).
 """
 
-from . import dense, ring  # noqa: F401
+from . import dense, layer, ring  # noqa: F401

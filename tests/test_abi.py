@@ -1,5 +1,5 @@
 """The C-ABI library loads, exports exactly what include/longctx100m_attn.h
-declares, and rejects bad arguments with the reference's messages
+and include/longctx100m_layer.h declare, and rejects bad arguments with the reference's messages
 (rust/longctx100m-model/src/ring_attention.rs:148-171) before touching the
 GPU.  Runs without a GPU: no compute entry point is reached."""
 
@@ -11,13 +11,16 @@ import pytest
 
 from longctx100m_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "longctx100m_attn.h"
+HEADERS = [Path(__file__).resolve().parents[1] / "include" / name
+           for name in ("longctx100m_attn.h", "longctx100m_layer.h")]
 
 
 def header_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(lc_\w+)\s*\(", text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(lc_\w+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -38,6 +41,7 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.Shape) == 32
     assert ctypes.sizeof(_lib.Mask) == 32
     assert ctypes.sizeof(_lib.RingDesc) == 64
+    assert ctypes.sizeof(_lib.Rope) == 56
     assert _lib.RingDesc.valid_length.offset == 48
 
 

@@ -1,0 +1,176 @@
+"""GPU parity of the decoder-layer row kernels (include/longctx100m_layer.h)
+and of one composed layer against the numpy oracle (oracle/layer.py, with
+oracle/dense.py for the attention).
+
+Bars: bf16 results within one bf16 ulp of the oracle (2^-7 relative, the two
+roundings the reference makes can each land on the other side), fp32 within
+2e-6 relative; RoPE given the same table and the fused residual add are
+bit-exact; the composed bf16 layer within 2e-2 norm-relative.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import dense
+from oracle import layer as L
+from tests.conftest import norm_rel
+
+pytestmark = pytest.mark.gpu
+
+BF16_ULP = 2.0 ** -7
+
+
+@pytest.fixture(scope="module")
+def ly(gpu):
+    from longctx100m_amd import layer
+
+    return layer
+
+
+def _t(gpu, arr, dtype):
+    return gpu.tensor(np.ascontiguousarray(arr), dtype=gpu.float32).to(dtype).cuda()
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _close(got, want, dtype):
+    if dtype == "bf16":
+        rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-30)
+        bad = (rel > BF16_ULP) & (np.abs(got - want) > 1e-30)
+        assert not bad.any(), (got[bad][:5], want[bad][:5])
+    else:
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
+
+
+def _dt(gpu, name):
+    return gpu.bfloat16 if name == "bf16" else gpu.float32
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("rows,cols,with_res", [(37, 4096, False), (64, 1000, True), (5, 16384, True)])
+def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 2
+    r = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(cols)).astype(np.float32)
+    if dtype == "bf16":
+        x, r, w = L.bf16(x), L.bf16(r), L.bf16(w)
+    tdt = _dt(gpu, dtype)
+    # x as a strided view (row stride cols + 16)
+    xbig = _t(gpu, np.pad(x, ((0, 0), (0, 16))), tdt)
+    xv = xbig[:, :cols]
+    tw = _t(gpu, w, tdt)
+    if with_res:
+        tr = _t(gpu, r, tdt)
+        hout = gpu.empty_like(xbig)
+        out = ly.rmsnorm(xv, tw, 1e-5, residual=tr, residual_out=hout[:, :cols])
+        want, h = L.rmsnorm(x, w, 1e-5, residual=r, dtype=dtype)
+        np.testing.assert_array_equal(_np(hout[:, :cols]), h)
+    else:
+        out = ly.rmsnorm(xv, tw, 1e-5)
+        want, _ = L.rmsnorm(x, w, 1e-5, dtype=dtype)
+    gpu.cuda.synchronize()
+    _close(_np(out), want, dtype)
+
+
+@pytest.mark.parametrize("scaling", [None, {"rope_type": "linear", "factor": 4.0},
+                                     {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                                      "high_freq_factor": 4.0,
+                                      "original_max_position_embeddings": 8192,
+                                      "attention_factor": 1.25}])
+def test_rope_table(ly, gpu, scaling):
+    d, theta, n, pos0 = 128, 500000.0, 700, 3 * 65536 - 300
+    rope = ly.rope_params(d, theta, scaling)
+    tab = _np(ly.rope_table(rope, n, pos0))
+    kw = {}
+    if scaling:
+        kw = {k: v for k, v in scaling.items() if k != "rope_type"}
+        kw["rope_type"] = scaling["rope_type"]
+    inv, cf, ps = L.rope_inv_freq(d, theta, **kw)
+    want = L.rope_table(inv, cf, ps, n, pos0)
+    # the same fp32 angle; device and host cos/sin agree to a couple of ulp
+    np.testing.assert_allclose(tab, want, rtol=0, atol=4e-7)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_rope_apply_strided_and_in_place(ly, gpu, dtype):
+    rng = np.random.default_rng(5)
+    T, hq, hkv, d = 96, 6, 2, 128
+    tdt = _dt(gpu, dtype)
+    qkv = rng.standard_normal((T, (hq + 2 * hkv) * d)).astype(np.float32)
+    if dtype == "bf16":
+        qkv = L.bf16(qkv)
+    tq = _t(gpu, qkv, tdt)
+    rope = ly.rope_params(d, 500000.0)
+    table = ly.rope_table(rope, T, 12345)
+    q = ly.rope_apply(tq[:, :hq * d], table, hq, d)
+    k = ly.rope_apply(tq[:, hq * d:(hq + hkv) * d], table, hkv, d)
+    gtab = _np(table)
+    np.testing.assert_array_equal(_np(q), L.rope_apply(qkv[:, :hq * d].reshape(T, hq, d), gtab, dtype=dtype))
+    np.testing.assert_array_equal(_np(k), L.rope_apply(qkv[:, hq * d:(hq + hkv) * d].reshape(T, hkv, d), gtab, dtype=dtype))
+    # in place on a contiguous tensor
+    kc = _t(gpu, qkv[:, hq * d:(hq + hkv) * d], tdt)
+    ly.rope_apply(kc, table, hkv, d, out=kc.view(T, hkv, d))
+    np.testing.assert_array_equal(_np(kc).reshape(T, hkv, d), _np(k))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_swiglu(ly, gpu, dtype):
+    rng = np.random.default_rng(6)
+    rows, inter = 33, 2048
+    gu = (rng.standard_normal((rows, 2 * inter)) * 4).astype(np.float32)
+    gu[0, :4] = [-120.0, 120.0, 0.0, -0.0]
+    if dtype == "bf16":
+        gu = L.bf16(gu)
+    t = _t(gpu, gu, _dt(gpu, dtype))
+    out = ly.swiglu(t[:, :inter], t[:, inter:])
+    gpu.cuda.synchronize()
+    _close(_np(out), L.swiglu(gu[:, :inter], gu[:, inter:], dtype=dtype), dtype)
+
+
+def test_layer_prefill_reduced(ly, gpu):
+    """One decoder layer (hidden 1024, GQA 8/2, d 128, intermediate 2048, bf16)
+    on rank 1 of a 2-rank ring, 256 tokens per shard, against the oracle
+    composition (GEMMs in fp32 on the bf16 operands, rounded to bf16)."""
+    import torch
+
+    cfg = ly.ModelConfig(hidden_size=1024, num_heads=8, num_key_value_heads=2,
+                         intermediate_size=2048, num_layers=1, rope_theta=500000.0)
+    T, rank, d = 256, 1, cfg.head_dim
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    w = ly.init_layer_weights(cfg, gen, "cuda", std=0.05)
+    w["norm1"] = (1 + 0.1 * torch.randn(1024, generator=gen, device="cuda")).to(torch.bfloat16)
+    w["norm2"] = (1 + 0.1 * torch.randn(1024, generator=gen, device="cuda")).to(torch.bfloat16)
+    x = torch.randn(T, 1024, generator=gen, device="cuda").to(torch.bfloat16)
+    res = (0.5 * torch.randn(T, 1024, generator=gen, device="cuda")).to(torch.bfloat16)
+    pk = torch.randn(1, T, 2, d, generator=gen, device="cuda").to(torch.bfloat16)
+    pv = torch.randn(1, T, 2, d, generator=gen, device="cuda").to(torch.bfloat16)
+    table = ly.rope_table(ly.rope_params(d, cfg.rope_theta), T, rank * T)
+    x2, mlp = ly.layer_prefill(x, w, cfg, table, rank, [(pk, pv)], residual=res)
+    gpu.cuda.synchronize()
+
+    W = {k: _np(v) for k, v in w.items()}
+    xn, rn = _np(x), _np(res)
+    gtab = _np(table)
+
+    def gemm(a, b):  # a @ b.T, fp32 accumulate, bf16 result
+        return L.bf16(a.astype(np.float64) @ b.astype(np.float64).T)
+
+    h, xin = L.rmsnorm(xn, W["norm1"], cfg.rms_norm_eps, residual=rn)
+    qkv = gemm(h, W["wqkv"])
+    q = L.rope_apply(qkv[:, :8 * d].reshape(T, 8, d), gtab)
+    k = L.rope_apply(qkv[:, 8 * d:10 * d].reshape(T, 2, d), gtab)
+    v = qkv[:, 10 * d:].reshape(T, 2, d)
+    kall = np.concatenate([_np(pk)[0], k], 0)[None]
+    vall = np.concatenate([_np(pv)[0], v], 0)[None]
+    att = L.bf16(dense.attention_fwd(q[None], kall, vall, q_pos0=rank * T, k_pos0=0)[0][0])
+    o = gemm(att.reshape(T, 8 * d), W["wo"])
+    h2, x2w = L.rmsnorm(xin, W["norm2"], cfg.rms_norm_eps, residual=o)
+    gu = gemm(h2, W["wgu"])
+    a = L.swiglu(gu[:, :2048], gu[:, 2048:])
+    mlpw = gemm(a, W["wd"])
+    assert norm_rel(_np(x2), x2w) <= 2e-2
+    assert norm_rel(_np(mlp), mlpw) <= 2e-2
