@@ -82,6 +82,22 @@ typedef struct lc_attn_mask {
 int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
                       const void* k, const void* v, float* o, float* m, float* l, void* stream);
 
+/* Split-KV decode: the same outputs as lc_attn_fwd_shard for a query shard of
+ * a few tokens against a long KV shard (a decode step over a KV cache).  For
+ * bf16, head_dim 128 and q_tokens * heads_q / heads_kv <= 16 the key range of
+ * each (batch, KV head) is split over many one-wave workgroups that stream the
+ * cache, and a second kernel merges the splits by log-sum-exp; it needs a
+ * workspace of lc_attn_decode_workspace_bytes(shape) bytes.  Other shapes run
+ * the lc_attn_fwd_shard kernels (workspace unused; the size query returns 0).
+ * No counterpart in the reference, whose generation loops recompute the whole
+ * prefill for every new token (src/longctx100m/distributed_infer.py:185-219,
+ * rust/longctx100m-model/src/bin/infer.rs:96-106); callers that keep a KV cache
+ * use it in place of that recomputation. */
+size_t lc_attn_decode_workspace_bytes(const lc_attn_shape_t* shape);
+int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                   const void* k, const void* v, float* o, float* m, float* l, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* Log-sum-exp merge of a partial (o_part, m_part, l_part) into the running
  * state (o_run, m_run, l_run), in place -- the carried (m, l, acc) state of
  * the reference's hop loop (rs:195-225).  If out != NULL the merged result is

@@ -86,6 +86,9 @@ _S, _M, _R = POINTER(Shape), POINTER(Mask), POINTER(RingDesc)
 SIGNATURES = {
     "lc_attn_fwd_shard": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p]),
+    "lc_attn_decode_workspace_bytes": (c_size_t, [_S]),
+    "lc_attn_decode": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                               c_void_p, c_void_p, c_size_t, c_void_p]),
     "lc_attn_merge": (c_int, [_S, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p]),
     "lc_attn_init_state": (c_int, [_S, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -235,6 +235,37 @@ int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
   return fwd_shard(p, q, k, v, o, m, l, st);
 }
 
+size_t lc_attn_decode_workspace_bytes(const lc_attn_shape_t* shape) {
+  if (check_shape(shape) != LC_OK) return 0;
+  const lc::Problem p = make_problem(shape, nullptr);
+  return lc::decode_supported(p) ? round_up(lc::decode_workspace_bytes(p)) : 0;
+}
+
+int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                   const void* k, const void* v, float* o, float* m, float* l, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (mask && mask->valid_length < -1)
+    return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
+  const lc::Problem p = make_problem(shape, mask);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p.Nq == 0) return LC_OK;
+  if (!pair_active(p)) {
+    hipError_t e = lc::launch_init_state(p.B, p.Nq, p.Hq, p.D, o, m, l, st);
+    return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode init");
+  }
+  if (!lc::decode_supported(p) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      !aligned16(o))
+    return fwd_shard(p, q, k, v, o, m, l, st);  // the blockwise kernels, no workspace
+  const size_t need = round_up(lc::decode_workspace_bytes(p));
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(LC_ERR_WORKSPACE, "decode workspace of %zu bytes is smaller than %zu",
+                     workspace_bytes, need);
+  hipError_t e = lc::launch_decode128(p, q, k, v, o, m, l, workspace, st);
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode launch");
+}
+
 int lc_attn_merge(const lc_attn_shape_t* shape, float* o_run, float* m_run, float* l_run,
                   const float* o_part, const float* m_part, const float* l_part, void* out,
                   void* stream) {

@@ -1,0 +1,280 @@
+// Split-KV decode attention for head_dim 128 on bf16 MFMA (gfx950): a few new
+// query tokens against a long KV cache.
+//
+// Same semantics and outputs as the blockwise forward of one ring hop
+// (rust/longctx100m-model/src/ring_attention.rs:15-106 and the finalize of
+// :227): normalised o [B, Nq, Hq, D] fp32 and the row statistics m, l.  The
+// work split is the decode one: each (batch, KV head) has R = Nq * group
+// query rows (group = Hq / Hkv, R <= 16: one MFMA column block), so the
+// key range is split over S one-wave workgroups that stream the cache, each
+// leaving a partial (o, m, l) in the workspace; decode_merge_kernel combines
+// the S partials by log-sum-exp.
+//
+// Per wave: Q^T of the R rows in VGPRs (B operand, rows >= R are zero);
+// 32-key tiles of K and V double-buffered in LDS by direct global->LDS loads
+// (tile128.h layout); S^T = K Q^T, exact online softmax per row in the log2
+// domain, O^T += V^T P^T with V^T from transposed LDS reads.
+#include "common.h"
+#include "kernels.h"
+#include "tile128.h"
+
+#include <type_traits>
+
+namespace lc {
+namespace {
+
+constexpr int D = 128;
+constexpr int TK = 32;  // keys per tile
+constexpr int KS = D / 32;
+constexpr int DB = D / 16;
+constexpr int kTileBytes = TK * t128::kRowBytes;
+
+struct DecodeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  float* o_part;  // [S][B*Nq*Hq][D]
+  float* m_part;  // [S][B*Nq*Hq]
+  float* l_part;
+  int Nq, Nk, Hq, Hkv, group, rows, S, chunk;  // chunk: keys per split (multiple of TK)
+  int64_t prows;                               // B * Nq * Hq: rows of one split's partial
+  int64_t q_pos0, k_pos0, valid;
+  int causal;
+  float sl2;  // scale * log2(e)
+};
+
+__global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
+
+  const int lane = threadIdx.x;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int s = blockIdx.x % a.S;
+  const int bh = blockIdx.x / a.S;
+  const int hk = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+
+  const int64_t ks = (int64_t)a.Hkv * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+
+  // Keys any row can see, then this split's share of them.
+  int64_t kend = a.Nk;
+  if (a.causal) kend = min(kend, a.q_pos0 + a.Nq - a.k_pos0);
+  kend = min(kend, a.valid - a.k_pos0);
+  const int64_t kb0 = (int64_t)s * a.chunk;
+  const int64_t kb1 = min(kb0 + a.chunk, kend);
+  const int ntiles = kb1 > kb0 ? (int)((kb1 - kb0 + TK - 1) / TK) : 0;
+
+  t128::RowLoader<TK, 1> ld;
+  ld.init(ks, 0, lane);
+  if (ntiles > 0) {
+    ld.load(kbase, ks, (int)kb0, a.Nk, kbuf[0], 0, lane);
+    ld.load(vbase, ks, (int)kb0, a.Nk, vbuf[0], 0, lane);
+  }
+
+  // Row c of this (batch, KV head): query head hk*group + c / Nq, query c % Nq.
+  const bool row_ok = c < a.rows;
+  const int qi = row_ok ? c % a.Nq : 0;
+  const int qh = hk * a.group + (row_ok ? c / a.Nq : 0);
+  const int64_t qpos = a.q_pos0 + qi;
+  bf16x8 qreg[KS];
+  {
+    const uint16_t* qrow = a.q + (((int64_t)b * a.Nq + qi) * a.Hq + qh) * D;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      qreg[kk] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kk + 8 * g);
+      if (!row_ok) qreg[kk] = bf16x8{};
+    }
+  }
+
+  int koff[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) koff[kk] = t128::row_chunk_off(c, 4 * kk + g);
+  int voff[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) voff[db] = t128::tr_off(0, 16 * db, lane);
+
+  f32x4 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -INFINITY;  // running max of this lane's row (log2 units)
+  float lsum = 0.f;        // lane-partial sum of p
+
+  for (int j = 0; j < ntiles; ++j) {
+    t128::wait_vmem();
+    if (j + 1 < ntiles) {
+      ld.load(kbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, kbuf[(j + 1) & 1], 0, lane);
+      ld.load(vbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, vbuf[(j + 1) & 1], 0, lane);
+    }
+    const uint8_t* kt = kbuf[j & 1];
+    const uint8_t* vt = vbuf[j & 1];
+    const int64_t key0 = kb0 + (int64_t)j * TK;
+
+    f32x4 sc[2];
+    sc[0] = sc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kt + koff[kk] + mb * 16 * t128::kRowBytes);
+        sc[mb] = mfma16x16x32(ka, qreg[kk], sc[mb]);
+      }
+    }
+    // Mask: past the split / cache end, valid_length, causal (per row).
+    const int64_t kmax = kb1 - key0;  // keys of this tile inside the split
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = 16 * mb + 4 * g + i;
+        const int64_t kp = a.k_pos0 + key0 + kr;
+        const bool bad = kr >= kmax || (a.causal && kp > qpos);
+        sc[mb][i] = bad ? -INFINITY : sc[mb][i] * a.sl2;
+      }
+    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mx = group4_max(mx);
+    if (mx > mrow) {
+      const float alpha = fast_exp2(mrow - mx);  // mrow = -inf: 0
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      mrow = mx;
+    }
+    const float muse = mrow == -INFINITY ? 0.f : mrow;  // no key yet: p = 0
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(sc[mb][i] - muse);
+        lsum += p;
+        sc[mb][i] = p;
+      }
+    const bf16x8 pb = pack_bf16x8(sc[0], sc[1]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const uint8_t* p = vt + voff[db];
+      const bf16x8 va = concat_bf16x4(t128::ds_read_tr(p), t128::ds_read_tr(p + 16 * t128::kRowBytes));
+      o[db] = mfma16x16x32(va, pb, o[db]);
+    }
+  }
+
+  // Partial of this split: normalised o, m (natural log), l.
+  const float lt = group4_sum(lsum);
+  if (row_ok) {
+    const int64_t row = ((int64_t)b * a.Nq + qi) * a.Hq + qh;
+    const int64_t prow = (int64_t)s * a.prows + row;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float* orow = a.o_part + prow * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+    if (g == 0) {
+      a.m_part[prow] = mrow == -INFINITY ? -INFINITY : mrow * kLn2;
+      a.l_part[prow] = lt;
+    }
+  }
+}
+
+// Log-sum-exp merge of the S split partials of each row: one wave per row
+// (b, i, h) = ((b * Nq) + i) * Hq + h of o, two head dims per lane; m and l
+// are written in the [B, Hq, Nq] layout of the statistics.
+__global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S, int Nq, int Hq,
+                                                           const float* o_part,
+                                                           const float* m_part,
+                                                           const float* l_part, float* o,
+                                                           float* m, float* l) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= nrows) return;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, m_part[(int64_t)s * nrows + row]);
+  float L = 0.f, acc0 = 0.f, acc1 = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < S; ++s) {
+      const int64_t pr = (int64_t)s * nrows + row;
+      const float ls = l_part[pr];
+      if (ls > 0.f) {
+        const float w = ls * expf(m_part[pr] - M);
+        const float2 ov = *reinterpret_cast<const float2*>(o_part + pr * D + 2 * lane);
+        acc0 = fmaf(w, ov.x, acc0);
+        acc1 = fmaf(w, ov.y, acc1);
+        L += w;
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  *reinterpret_cast<float2*>(o + row * D + 2 * lane) = float2{acc0 * inv, acc1 * inv};
+  if (lane == 0) {
+    const int h = (int)(row % Hq);
+    const int64_t bi = row / Hq;
+    const int64_t si = (bi / Nq * Hq + h) * Nq + bi % Nq;
+    m[si] = L > 0.f ? M : -INFINITY;
+    l[si] = L;
+  }
+}
+
+}  // namespace
+
+// Splits per (batch, KV head): enough one-wave workgroups to keep every CU's
+// LDS busy with cache tiles in flight, at least two tiles per split.
+int decode_splits(const Problem& p) {
+  const int64_t tiles = ((int64_t)p.Nk + TK - 1) / TK;
+  const int64_t want = (5 * 256 + (int64_t)p.B * p.Hkv - 1) / ((int64_t)p.B * p.Hkv);
+  int64_t s = want < 1 ? 1 : want;
+  const int64_t max_s = tiles / 2 < 1 ? 1 : tiles / 2;
+  if (s > max_s) s = max_s;
+  return (int)s;
+}
+
+bool decode_supported(const Problem& p) {
+  return p.dtype == 1 && !p.precise && p.D == D && (int64_t)p.Nq * (p.Hq / p.Hkv) <= 16;
+}
+
+size_t decode_workspace_bytes(const Problem& p) {
+  const int64_t rows = (int64_t)p.B * p.Nq * p.Hq;
+  const int64_t S = decode_splits(p);
+  return (size_t)(S * rows * D * 4 + 2 * S * rows * 4);
+}
+
+hipError_t launch_decode128(const Problem& p, const void* q, const void* k, const void* v,
+                            float* o, float* m, float* l, void* ws, hipStream_t st) {
+  if (!decode_supported(p)) return hipErrorInvalidValue;
+  const int S = decode_splits(p);
+  const int64_t rows = (int64_t)p.B * p.Nq * p.Hq;
+  float* o_part = static_cast<float*>(ws);
+  float* m_part = o_part + (int64_t)S * rows * D;
+  float* l_part = m_part + (int64_t)S * rows;
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o_part = o_part;
+  a.m_part = m_part;
+  a.l_part = l_part;
+  a.Nq = p.Nq;
+  a.Nk = p.Nk;
+  a.Hq = p.Hq;
+  a.Hkv = p.Hkv;
+  a.group = p.Hq / p.Hkv;
+  a.rows = p.Nq * a.group;
+  a.S = S;
+  a.prows = rows;
+  const int64_t per = ((int64_t)p.Nk + S - 1) / S;
+  a.chunk = (int)((per + TK - 1) / TK * TK);
+  a.q_pos0 = p.q_pos0;
+  a.k_pos0 = p.k_pos0;
+  a.valid = p.valid;
+  a.causal = p.causal ? 1 : 0;
+  a.sl2 = p.scale * kLog2e;
+  hipLaunchKernelGGL(decode128_kernel, dim3((unsigned)(S * p.Hkv * p.B)), dim3(64), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                     rows, S, p.Nq, p.Hq, o_part, m_part, l_part, o, m, l);
+  return hipGetLastError();
+}
+
+}  // namespace lc

@@ -74,6 +74,13 @@ hipError_t launch_bwd_preprocess(int B, int N, int H, int D, int dtype, const vo
                                  const void* dout, const float* m, const float* l, float* delta,
                                  float* lse2, hipStream_t s);
 
+// Split-KV decode attention (decode.hip): bf16, D = 128, Nq * Hq / Hkv <= 16.
+bool decode_supported(const Problem& p);
+int decode_splits(const Problem& p);
+size_t decode_workspace_bytes(const Problem& p);
+hipError_t launch_decode128(const Problem& p, const void* q, const void* k, const void* v,
+                            float* o, float* m, float* l, void* ws, hipStream_t s);
+
 // Decoder-layer row kernels (layer.hip).
 hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
                           int64_t xs, const void* res, int64_t rs, void* res_out, const void* w,

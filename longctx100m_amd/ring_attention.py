@@ -24,6 +24,7 @@ there is no CPU or PyTorch fallback.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -89,6 +90,29 @@ def fwd_shard(q, k, v, *, q_pos0: int, k_pos0: int, causal: bool = True,
     mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
     _lib.check(_lib.load().lc_attn_fwd_shard(s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                              o.data_ptr(), m.data_ptr(), l.data_ptr(), _stream()))
+    return o, m, l
+
+
+def decode(q, k, v, *, q_pos0: int, k_pos0: int = 0, causal: bool = True,
+           valid_length: Optional[int] = None, o: Optional[torch.Tensor] = None,
+           m: Optional[torch.Tensor] = None, l: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None):
+    """Split-KV decode of a few query tokens against a long KV shard (a KV
+    cache): same outputs as fwd_shard, (o [B,Nq,Hq,D] fp32, m, l [B,Hq,Nq])."""
+    _check_dev(q, k, v)
+    s = _shape(q, k, False)
+    mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
+    b, nq, hq, d = q.shape
+    o = torch.empty((b, nq, hq, d), dtype=torch.float32, device=q.device) if o is None else o
+    m = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if m is None else m
+    l = torch.empty_like(m) if l is None else l
+    lib = _lib.load()
+    need = lib.lc_attn_decode_workspace_bytes(ctypes.byref(s))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.lc_attn_decode(ctypes.byref(s), ctypes.byref(mk), q.data_ptr(), k.data_ptr(),
+                                  v.data_ptr(), o.data_ptr(), m.data_ptr(), l.data_ptr(),
+                                  workspace.data_ptr(), workspace.numel(), _stream()))
     return o, m, l
 
 
