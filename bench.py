@@ -55,6 +55,8 @@ def parse():
                          "rank 3 of 4, forward) instead of the default workload")
     ap.add_argument("--c4-model", action="store_true",
                     help="time the whole C4 model prefill share (embedding, 24 layers, LM head)")
+    ap.add_argument("--c4-decode", action="store_true",
+                    help="time incremental decode of the C4 model against a 262,144-token KV cache")
     ap.add_argument("--long-shard", action="store_true",
                     help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
                          "against its diagonal block plus one full incoming 1M-token KV shard; "
@@ -328,6 +330,92 @@ def c4_model(args, torch, ra) -> int:
     return 0
 
 
+def c4_decode(args, torch, ra) -> int:
+    """Incremental decode of the C4 model on one GPU: one new token against a
+    KV cache of 262,144 tokens per layer (the 4 x 65,536-token context of
+    config 4), through embedding, 24 layers (GEMVs, RoPE, split-KV decode
+    attention over the cache, SwiGLU) and the LM head.  The reference
+    recomputes the full prefill for every generated token
+    (distributed_infer.py:185-219, bin/infer.rs:96-106); this is the KV-cache
+    step that replaces it.  Cache contents and weights are seeded random."""
+    from longctx100m_amd import layer as ly
+
+    cfg = ly.C4
+    ctx, d, hkv = 4 * 65536, cfg.head_dim, cfg.num_key_value_heads
+    steps = max(1, args.steps)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(97531)
+    torch.cuda.reset_peak_memory_stats()
+    log(f"C4 decode: {cfg.num_layers} layers, KV cache of {ctx} tokens per layer")
+    weights = ly.init_model_weights(cfg, gen, dev)
+    cap = ctx + steps + max(0, args.warmup) + 1
+    caches = []
+    for _ in range(cfg.num_layers):
+        caches.append(tuple(torch.randn(1, cap, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+                            for _ in range(2)))
+    table = ly.rope_table(ly.rope_params(d, cfg.rope_theta, cfg.rope_scaling), cap, 0)
+    q = torch.zeros(1, 1, cfg.num_heads, d, device=dev, dtype=torch.bfloat16)
+    sh = ra._shape(q, caches[0][0], False)
+    import ctypes as _ct
+    ws = torch.empty(max(1, ra._lib.load().lc_attn_decode_workspace_bytes(_ct.byref(sh))),
+                     dtype=torch.uint8, device=dev)
+    log("C4 decode: weights and caches ready")
+    pos = ctx
+    for _ in range(max(0, args.warmup)):
+        ly.model_decode_step(7, pos, weights, cfg, table, caches, ws)
+        pos += 1
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        logits = ly.model_decode_step(11 + i, pos, weights, cfg, table, caches, ws)
+        pos += 1
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    # the decode attention of one layer alone, at the same context
+    qx = torch.randn(1, 1, cfg.num_heads, d, generator=gen, device=dev).to(torch.bfloat16)
+    kc, vc = caches[0][0][:, :pos], caches[0][1][:, :pos]
+    ra.decode(qx, kc, vc, q_pos0=pos - 1, workspace=ws)
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    a0.record()
+    for _ in range(reps):
+        ra.decode(qx, kc, vc, q_pos0=pos - 1, workspace=ws)
+    a1.record()
+    torch.cuda.synchronize()
+    att_ms = a0.elapsed_time(a1) / reps
+    att_bytes = 2.0 * pos * hkv * d * 2
+    wbytes = sum(t.numel() * t.element_size() for lw in weights["layers"] for t in lw.values()) + \
+        weights["lm_head"].numel() * 2 + cfg.hidden_size * 2
+    cache_bytes = cfg.num_layers * att_bytes
+    line = {
+        "metric": "C4 decode ms per token (one GPU, 262,144-token KV cache per layer)",
+        "value": round(ms, 3), "unit": "ms/token", "n_gpus": 1, "steps": steps,
+        "ms_per_step": round(ms, 3), "higher_is_better": False,
+        "tokens_per_s": round(1e3 / ms, 1),
+        "dtype": "bf16", "data": "synthetic: seeded random weights N(0,0.02) and KV cache N(0,1)",
+        "config": {"workload": "config 4 model, incremental decode of one token at context "
+                               "262,144 (24 layers, GQA 32/8, d=128)", "context": ctx,
+                   "layers": cfg.num_layers},
+        "hbm_bytes_per_token": {"kv_cache": cache_bytes, "weights": wbytes},
+        "roofline": {"bound": "hbm", "achieved": round((cache_bytes + wbytes) / (ms * 1e-3) / 1e9, 1),
+                     "peak": 8000.0, "unit": "GB/s",
+                     "frac": round((cache_bytes + wbytes) / (ms * 1e-3) / 8e12, 4),
+                     "traffic": None, "kernel": "whole decode step (cache + weight reads)"},
+        "decode_attention_one_layer": {"ms": round(att_ms, 4), "bytes": att_bytes,
+                                       "GB_per_s": round(att_bytes / (att_ms * 1e-3) / 1e9, 1)},
+        "vs_prefill_recompute_ms": "the reference's loop reruns the 65,536-token prefill share per token "
+                                   "(bench.py --c4-model)",
+        "logits_shape": list(logits.shape),
+        "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -354,6 +442,8 @@ def main() -> int:
         return c4_prefill(args, torch, ra)
     if args.c4_model:
         return c4_model(args, torch, ra)
+    if args.c4_decode:
+        return c4_decode(args, torch, ra)
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")

@@ -171,11 +171,13 @@ def layer_prefill(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
                   table: torch.Tensor, rank: int,
                   preceding_kv: Sequence[Tuple[torch.Tensor, torch.Tensor]],
                   residual: Optional[torch.Tensor] = None,
-                  timers: Optional[Dict[str, list]] = None):
+                  timers: Optional[Dict[str, list]] = None,
+                  cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
     """One decoder layer over this rank's shard x [T, hidden].
 
     ``preceding_kv`` holds the (k, v) [1, T, Hkv, d] shards of ranks 0..rank-1
-    (the ring's incoming KV).  ``residual``, when given, is the previous
+    (the ring's incoming KV).  ``cache``, when given, is this layer's KV cache
+    ([1, capacity, Hkv, d] K and V) and receives the shard's rotated K and V.  ``residual``, when given, is the previous
     layer's MLP output still to be added to x (the add is fused into this
     layer's first RMSNorm).  Returns (x_after_attention, mlp_out): the layer
     output is their sum, which the next layer's (or the final) RMSNorm forms."""
@@ -205,6 +207,9 @@ def layer_prefill(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
     v = qkv[:, (hq + hkv) * d:].contiguous().view(T, hkv, d)
     tick("rope")
     qb, kb, vb = q.view(1, T, hq, d), k.view(1, T, hkv, d), v.view(1, T, hkv, d)
+    if cache is not None:  # keep this shard's rotated K and V for incremental decode
+        cache[0][:, :T].copy_(kb)
+        cache[1][:, :T].copy_(vb)
     shards = [(qb, pk, pv) for pk, pv in preceding_kv] + [(qb, kb, vb)]
     attn, _, _ = ra.ring_causal_attention_forward_with_stats(shards, rank)
     tick("attention")
@@ -231,3 +236,88 @@ def layer_flops(cfg: ModelConfig, tokens: int, rank: int) -> Dict[str, float]:
     gemm = 2.0 * tokens * c * ((hq + 2 * hkv) * d + hq * d + 2 * inter) + 2.0 * tokens * inter * c
     attn = (rank + 0.5) * 4.0 * tokens * tokens * hq * d
     return {"gemm": gemm, "attention": attn}
+
+
+# ------------------------------------------------------- incremental decode --
+
+def layer_decode(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
+                 table: torch.Tensor, pos: int, cache: Tuple[torch.Tensor, torch.Tensor],
+                 residual: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None):
+    """One decoder layer for the token at position ``pos`` (x [1, hidden]),
+    attending to the cache rows 0..pos after appending its own K and V.  The
+    reference recomputes the whole prefill for each new token
+    (src/longctx100m/distributed_infer.py:185-219,
+    rust/longctx100m-model/src/bin/infer.rs:96-106); this computes the same
+    last-position result from the cache.  ``table`` row ``pos`` holds the
+    token's RoPE angles.  Returns (x_after_attention, mlp_out) as layer_prefill."""
+    d, hq, hkv = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    if residual is not None:
+        xin = torch.empty_like(x)
+        h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps, residual=residual, residual_out=xin)
+    else:
+        xin = x
+        h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps)
+    qkv = torch.matmul(h, w["wqkv"].t())
+    trow = table[pos:pos + 1]
+    q = rope_apply(qkv[:, :hq * d], trow, hq, d)
+    kc, vc = cache
+    rope_apply(qkv[:, hq * d:(hq + hkv) * d], trow, hkv, d, out=kc[0, pos:pos + 1])
+    vc[0, pos:pos + 1].copy_(qkv[:, (hq + hkv) * d:].view(1, hkv, d))
+    o, _, _ = ra.decode(q.view(1, 1, hq, d), kc[:, :pos + 1], vc[:, :pos + 1], q_pos0=pos,
+                        k_pos0=0, workspace=workspace)
+    attn = o.to(x.dtype).view(1, hq * d)  # the forward output in the model dtype
+    ao = torch.matmul(attn, w["wo"].t())
+    x2 = torch.empty_like(x)
+    h2 = rmsnorm(xin, w["norm2"], cfg.rms_norm_eps, residual=ao, residual_out=x2)
+    gu = torch.matmul(h2, w["wgu"].t())
+    inter = cfg.intermediate_size
+    a = swiglu(gu[:, :inter], gu[:, inter:])
+    return x2, torch.matmul(a, w["wd"].t())
+
+
+def new_cache(cfg: ModelConfig, capacity: int, device, dtype=torch.bfloat16):
+    """Per-layer (K, V) caches [1, capacity, Hkv, d]."""
+    shape = (1, capacity, cfg.num_key_value_heads, cfg.head_dim)
+    return [(torch.zeros(shape, device=device, dtype=dtype),
+             torch.zeros(shape, device=device, dtype=dtype)) for _ in range(cfg.num_layers)]
+
+
+def model_prefill(ids: torch.Tensor, weights: Dict, cfg: ModelConfig, table: torch.Tensor,
+                  caches=None) -> torch.Tensor:
+    """Logits [T, vocab] of a one-rank prefill (embedding, layers, final norm,
+    LM head), filling ``caches`` with each layer's rotated K and V if given."""
+    x = torch.nn.functional.embedding(ids, weights["embed"])
+    res = None
+    for li, lw in enumerate(weights["layers"]):
+        x, res = layer_prefill(x, lw, cfg, table, 0, [], residual=res,
+                               cache=caches[li] if caches is not None else None)
+    h = rmsnorm(x, weights["final_norm"], cfg.rms_norm_eps, residual=res)
+    return torch.matmul(h, weights["lm_head"].t())
+
+
+def model_decode_step(token: int, pos: int, weights: Dict, cfg: ModelConfig,
+                      table: torch.Tensor, caches, workspace=None) -> torch.Tensor:
+    """Logits [1, vocab] of the token at ``pos`` given caches holding 0..pos-1."""
+    dev = weights["embed"].device
+    x = torch.nn.functional.embedding(torch.tensor([token], device=dev), weights["embed"])
+    res = None
+    for li, lw in enumerate(weights["layers"]):
+        x, res = layer_decode(x, lw, cfg, table, pos, caches[li], residual=res,
+                              workspace=workspace)
+    h = rmsnorm(x, weights["final_norm"], cfg.rms_norm_eps, residual=res)
+    return torch.matmul(h, weights["lm_head"].t())
+
+
+def init_model_weights(cfg: ModelConfig, gen: torch.Generator, device, dtype=torch.bfloat16,
+                       std: float = 0.02) -> Dict:
+    """Random-init weights of the whole model (untied LM head)."""
+    def randn(*shape):
+        return (torch.randn(*shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+    return {
+        "embed": randn(cfg.vocab_size, cfg.hidden_size),
+        "lm_head": randn(cfg.vocab_size, cfg.hidden_size),
+        "final_norm": torch.ones(cfg.hidden_size, device=device, dtype=dtype),
+        "layers": [init_layer_weights(cfg, gen, device, dtype, std) for _ in range(cfg.num_layers)],
+    }

@@ -174,3 +174,30 @@ def test_layer_prefill_reduced(ly, gpu):
     mlpw = gemm(a, W["wd"])
     assert norm_rel(_np(x2), x2w) <= 2e-2
     assert norm_rel(_np(mlp), mlpw) <= 2e-2
+
+
+def test_decode_steps_match_prefill(ly, gpu):
+    """Incremental decode against the reference's generation semantics, which
+    recompute the whole prefill per new token and read the last position
+    (bin/infer.rs:96-106): a 2-layer model (hidden 512, GQA 4/2, d 128) is
+    prefilled on 300 tokens, then 4 tokens are decoded from the KV cache; each
+    step's logits equal the full prefill's logits at that position."""
+    import torch
+
+    cfg = ly.ModelConfig(hidden_size=512, num_heads=4, num_key_value_heads=2,
+                         intermediate_size=1024, num_layers=2, vocab_size=1000,
+                         rope_theta=500000.0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(21)
+    weights = ly.init_model_weights(cfg, gen, "cuda", std=0.05)
+    T, extra = 300, 4
+    ids = torch.randint(0, cfg.vocab_size, (T + extra,), generator=gen, device="cuda")
+    table = ly.rope_table(ly.rope_params(cfg.head_dim, cfg.rope_theta), T + extra, 0)
+    full = ly.model_prefill(ids, weights, cfg, table)
+    caches = ly.new_cache(cfg, T + extra, "cuda")
+    ly.model_prefill(ids[:T], weights, cfg, table[:T], caches)
+    for step in range(extra):
+        pos = T + step
+        logits = ly.model_decode_step(int(ids[pos]), pos, weights, cfg, table, caches)
+        gpu.cuda.synchronize()
+        assert norm_rel(_np(logits[0]), _np(full[pos])) <= 2e-2, step
