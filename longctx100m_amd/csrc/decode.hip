@@ -178,36 +178,66 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   }
 }
 
-// Log-sum-exp merge of the S split partials of each row: one wave per row
-// (b, i, h) = ((b * Nq) + i) * Hq + h of o, two head dims per lane; m and l
-// are written in the [B, Hq, Nq] layout of the statistics.
+// Log-sum-exp merge of the S split partials of each row: one 256-thread
+// workgroup per row (b, i, h) = ((b * Nq) + i) * Hq + h of o.  The split
+// weights w_s = l_s * exp(m_s - M) are formed in parallel over the splits,
+// then thread (d, half) sums w_s * o_s[d] over half of the splits, so the
+// partial reads are independent and stream.  m and l are written in the
+// [B, Hq, Nq] layout of the statistics.
+constexpr int kMergeMaxSplits = 4096;
+
 __global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S, int Nq, int Hq,
                                                            const float* o_part,
                                                            const float* m_part,
                                                            const float* l_part, float* o,
                                                            float* m, float* l) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= nrows) return;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, m_part[(int64_t)s * nrows + row]);
-  float L = 0.f, acc0 = 0.f, acc1 = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const int64_t pr = (int64_t)s * nrows + row;
-      const float ls = l_part[pr];
-      if (ls > 0.f) {
-        const float w = ls * expf(m_part[pr] - M);
-        const float2 ov = *reinterpret_cast<const float2*>(o_part + pr * D + 2 * lane);
-        acc0 = fmaf(w, ov.x, acc0);
-        acc1 = fmaf(w, ov.y, acc1);
-        L += w;
-      }
-    }
+  __shared__ float w[kMergeMaxSplits];
+  __shared__ float red[256];
+  __shared__ float half_acc[D];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  // M = max over splits
+  float mx = -INFINITY;
+  for (int s = t; s < S; s += 256) mx = fmaxf(mx, m_part[(int64_t)s * nrows + row]);
+  red[t] = mx;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) red[t] = fmaxf(red[t], red[t + off]);
+    __syncthreads();
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  *reinterpret_cast<float2*>(o + row * D + 2 * lane) = float2{acc0 * inv, acc1 * inv};
-  if (lane == 0) {
+  const float M = red[0];
+  __syncthreads();
+  // weights and L
+  float lsum = 0.f;
+  for (int s = t; s < S; s += 256) {
+    const int64_t pr = (int64_t)s * nrows + row;
+    const float ls = l_part[pr];
+    const float ws = (M == -INFINITY || !(ls > 0.f)) ? 0.f : ls * expf(m_part[pr] - M);
+    w[s] = ws;
+    lsum += ws;
+  }
+  red[t] = lsum;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) red[t] += red[t + off];
+    __syncthreads();
+  }
+  const float L = red[0];
+  // weighted sum of the partial outputs: thread (d, half)
+  const int d = t & (D - 1);
+  const int hf = t >> 7;  // 0 or 1
+  float acc = 0.f;
+  for (int s = hf; s < S; s += 2) {
+    const float ws = w[s];
+    if (ws != 0.f) acc = fmaf(ws, o_part[((int64_t)s * nrows + row) * D + d], acc);
+  }
+  if (hf == 1) half_acc[d] = acc;
+  __syncthreads();
+  if (hf == 0) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    o[row * D + d] = (acc + half_acc[d]) * inv;
+  }
+  if (t == 0) {
     const int h = (int)(row % Hq);
     const int64_t bi = row / Hq;
     const int64_t si = (bi / Nq * Hq + h) * Nq + bi % Nq;
@@ -226,6 +256,7 @@ int decode_splits(const Problem& p) {
   int64_t s = want < 1 ? 1 : want;
   const int64_t max_s = tiles / 2 < 1 ? 1 : tiles / 2;
   if (s > max_s) s = max_s;
+  if (s > kMergeMaxSplits) s = kMergeMaxSplits;
   return (int)s;
 }
 
@@ -272,7 +303,7 @@ hipError_t launch_decode128(const Problem& p, const void* q, const void* k, cons
   hipLaunchKernelGGL(decode128_kernel, dim3((unsigned)(S * p.Hkv * p.B)), dim3(64), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st,
                      rows, S, p.Nq, p.Hq, o_part, m_part, l_part, o, m, l);
   return hipGetLastError();
 }
