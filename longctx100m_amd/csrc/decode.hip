@@ -226,11 +226,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S,
   // weighted sum of the partial outputs: thread (d, half)
   const int d = t & (D - 1);
   const int hf = t >> 7;  // 0 or 1
-  float acc = 0.f;
-  for (int s = hf; s < S; s += 2) {
-    const float ws = w[s];
-    if (ws != 0.f) acc = fmaf(ws, o_part[((int64_t)s * nrows + row) * D + d], acc);
-  }
+  float acc = 0.f;  // partials of empty splits are zeros with zero weight
+  const float* op = o_part + row * D + d;
+  const int64_t sstride = 2 * nrows * D;
+#pragma unroll 8
+  for (int s = hf; s < S; s += 2) acc = fmaf(w[s], op[(int64_t)(s >> 1) * sstride + (int64_t)hf * nrows * D], acc);
   if (hf == 1) half_acc[d] = acc;
   __syncthreads();
   if (hf == 0) {
