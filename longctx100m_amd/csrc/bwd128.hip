@@ -95,8 +95,8 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 
   t128::RowLoader<kDqBN, 4> ld;
   ld.init(ks, wave, lane);
-  ld.load(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
-  ld.load(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+  ld.load<true>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
+  ld.load<true>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
 
   bf16x8 qreg[2][KS], doreg[2][KS];
   float lse[2], dl[2];
@@ -184,8 +184,8 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
     __syncthreads();
     if (j + 1 < ntiles) {
       const int nbuf = (j + 1) & 1;
-      ld.load(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
-      ld.load(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
+      ld.load<true>(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
+      ld.load<true>(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
     }
     const int key0 = j * kDqBN;
     const int64_t kp_first = a.k_pos0 + key0;
@@ -226,6 +226,43 @@ constexpr int kKvBN = 4 * kKvKW;  // keys per workgroup
 constexpr int kKvBM = 32;         // queries per tile
 constexpr int kKvTile = kKvBM * t128::kRowBytes;
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Byte offset of a transposed read for the 32x32x16 A operand X^T (X = a
+// [32 x 128] Q or dO tile; k index = query row, m index = column), column
+// block 0 and k-half p: lane l receives X[row(l/32, p, t)][l%32] in slot t,
+// with row(h, p, t) = 4h + p + 2(t%2) + 8(t/2).  The four rows read in one
+// cycle (lanes 0-31 or 32-63) then have distinct swz(r) / 4, so the 4 rows x
+// 4 chunks land on 16 distinct chunks (no bank conflict).  Column block dblk
+// is offset ^ (64 * dblk) (the block index occupies chunk bits 2-3 alone);
+// rows 16 .. 31 are offset + 16 * kRowBytes (swz depends on r % 16).
+__device__ __forceinline__ int tr32_off(int p, int lane) {
+  const int G = lane >> 4, i = lane & 15, t = i >> 2;
+  const int col = 16 * (G & 1) + 4 * (i & 3);
+  const int r = 4 * (G >> 1) + p + 2 * (t & 1) + 8 * (t >> 1);
+  return r * t128::kRowBytes + 16 * ((col >> 3) ^ t128::swz(r)) + 2 * (col & 7);
+}
+
+// Hides a value from loop-invariant code motion, so offsets derived from it
+// by an XOR are formed next to their use instead of occupying registers.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// dK/dV with v_mfma_f32_32x32x16_bf16: one 32x32 score block per wave and
+// query tile, so half the MFMA instructions of the 16x16x32 form.
+//   S = Q K^T, dP = dO V^T    A = Q, dO rows (ds_read_b128), B = K^T (VGPRs),
+//                             V^T (rows of the V tile)
+//   dV^T += dO^T P, dK^T += Q^T dS   A = dO^T, Q^T (transposed reads),
+//                             B = P, dS straight from the score accumulators
+// Score element v of lane l: query 8(v/4) + 4(l/32) + v%4, key l%32.  As a B
+// operand, k-step u (queries 16u .. 16u+15) takes, in slot 4p + t, element
+// 8u + 4(t/2) + 2(t%2) + p, i.e. query 16u + row(h, p, t) of tr32_off.
 __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kKvTile];  // [buf][Q,dO]
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kKvBN * t128::kRowBytes];
@@ -234,8 +271,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int c = lane & 15;
-  const int g = lane >> 4;
+  const int kc = lane & 31;  // key column of the wave's 32 keys
+  const int h = lane >> 5;
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int kt = L % a.n_tiles;  // early keys see the most queries: dispatched first
@@ -266,9 +303,6 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
 
   t128::RowLoader<kKvBM, 4> ld;
   ld.init(qs, wave, lane);
-  // Steps walk (query head of the group, query tile) with running counters
-  // (no integer division per step): step s covers head hk*group + s / ntq and
-  // query rows qstart + (s % ntq) * kKvBM.
   auto issue = [&](int hq, int qrow0, int buf) {
     const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
     const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
@@ -277,21 +311,17 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.Nq;
     if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, stat[buf][0], lane);
     if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, stat[buf][1], lane);
-    // (64 entries are fetched; the tile uses the first kKvBM)
   };
   const int hq0 = hk * a.group;
   issue(hq0, qstart, 0);
 
-  // K^T as B operand in VGPRs: lane holds key (16*nb + c), dims 32*kk + 8g .. +7.
-  // V^T, the B operand of dP, is read from an LDS tile of the workgroup's
-  // keys (keeps the kernel within 256 VGPRs, i.e. two workgroups per CU).
-  bf16x8 kreg[2][KS];
+  // K^T as the B operand in VGPRs: lane l holds key kw0 + l%32, dims 16t + 8h .. +7.
+  bf16x8 kreg[D / 16];
+  {
+    const int row = min(kw0 + kc, a.Nk - 1);
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int row = min(kw0 + 16 * nb + c, a.Nk - 1);
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-      kreg[nb][kk] = *reinterpret_cast<const bf16x8*>(kbase + (int64_t)row * ks + 32 * kk + 8 * g);
+    for (int t = 0; t < D / 16; ++t)
+      kreg[t] = *reinterpret_cast<const bf16x8*>(kbase + (int64_t)row * ks + 16 * t + 8 * h);
   }
   {
     t128::RowLoader<kKvBN, 4> vld;
@@ -299,93 +329,123 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     vld.load(vbase, ks, k0, a.Nk, v_lds, wave, lane);
   }
 
-  int roff[KS];
+  // Row l%32 of a Q/dO tile, dims 16t + 8h .. +7, is roff0 ^ (32 t); the
+  // wave's V rows are the same offsets in the wave's part of the V tile.
+  const int roff0 = t128::row_chunk_off(kc, h);
+  const int voff0 = roff0 + wave * kKvKW * t128::kRowBytes;
+  const int toff0 = tr32_off(0, lane), toff1 = tr32_off(1, lane);
+  f32x16 dk[4], dv[4];
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk) roff[kk] = t128::row_chunk_off(c, 4 * kk + g);
-  const int* voff = roff;  // V^T rows of the V tile: same (row c, chunk 4kk+g) map
-  int toff[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) toff[db] = t128::tr_off(0, 16 * db, lane);
-
-  f32x4 dk[DB][2], dv[DB][2];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-    dk[db][0] = dk[db][1] = dv[db][0] = dv[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) dk[i] = dv[i] = f32x16{};
 
   const int64_t wk_first = a.k_pos0 + kw0;
   const int64_t wk_last = wk_first + kKvKW - 1;
 
-  // One query tile, per 32-query half (kk2): S = Q K^T and dP = dO V^T for
-  // queries 32*kk2 + [16mb+4g+i] x key 16nb+c of the wave, then
-  // dV^T += dO^T P and dK^T += Q^T dS.  Mask (MASKED only): query q of the
-  // tile / key k of the wave are invalid when
-  // (causal && k - q > cthr) || k >= kmax || q >= qmax.
+  // One query tile as a stream of 32 MFMA steps j, each with its operands
+  // fetched from LDS two steps ahead (A[j&1], B[j&1]):
+  //   j  0- 7  S    += Q[:, 16t..]  K^T            (t = j)
+  //   j  8-15  dP   += dO[:, 16t..] V^T            (t = j - 8)
+  //   j 16-23  dV^T += dO^T P       (u, dblk) = ((j-16)/4, (j-16)%4)
+  //   j 24-31  dK^T += Q^T dS       (u, dblk) = ((j-24)/4, (j-24)%4)
+  // P = exp2(S sl2 - lse2) is formed on the VALU during the dP steps, and
+  // dS = P (dP - delta) during the dV steps, beside the running MFMAs.
   auto tile = [&](auto masked_tag, int buf, int cthr, int kmax, int qmax) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     const uint8_t* qt_ = smem[buf][0];
     const uint8_t* ot_ = smem[buf][1];
-    bf16x8 vb[2][KS];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk)
-        vb[nb][kk] = *reinterpret_cast<const bf16x8*>(v_lds + voff[kk] + (wave * 2 + nb) * 16 * t128::kRowBytes);
-#pragma unroll
-    for (int kk2 = 0; kk2 < kKvBM / 32; ++kk2) {
-      f32x4 s[2][2], dp[2][2];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        s[mb][0] = s[mb][1] = dp[mb][0] = dp[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const int off = roff[kk] + (2 * kk2 + mb) * 16 * t128::kRowBytes;
-          const bf16x8 qa = *reinterpret_cast<const bf16x8*>(qt_ + off);
-          const bf16x8 oa = *reinterpret_cast<const bf16x8*>(ot_ + off);
-          s[mb][0] = mfma16x16x32(qa, kreg[0][kk], s[mb][0]);
-          s[mb][1] = mfma16x16x32(qa, kreg[1][kk], s[mb][1]);
-          dp[mb][0] = mfma16x16x32(oa, vb[0][kk], dp[mb][0]);
-          dp[mb][1] = mfma16x16x32(oa, vb[1][kk], dp[mb][1]);
-        }
+    const float* lse_ = stat[buf][0];
+    const float* dlt_ = stat[buf][1];
+    const int ro = opaque(roff0), vo = opaque(voff0);
+    const int to0 = opaque(toff0), to1 = opaque(toff1);
+    auto ld = [](const uint8_t* p) { return *reinterpret_cast<const bf16x8*>(p); };
+    auto fetch = [&](int j, bf16x8& A, bf16x8& B) {
+      if (j < 8) {
+        A = ld(qt_ + (ro ^ (32 * j)));
+      } else if (j < 16) {
+        A = ld(ot_ + (ro ^ (32 * (j - 8))));
+        B = ld(v_lds + (vo ^ (32 * (j - 8))));
+      } else {
+        const uint8_t* src = j < 24 ? ot_ : qt_;
+        const int i = (j - 16) & 7;
+        const int o0 = (to0 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+        const int o1 = (to1 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+        A = concat_bf16x4(t128::ds_read_tr(src + o0), t128::ds_read_tr(src + o1));
       }
+    };
+    int kq = 0, qlim = 0;
+    bool kbad = false;
+    if constexpr (MASKED) {
+      kq = opaque(kc - 4 * h);
+      qlim = opaque(qmax - 4 * h);
+      kbad = kc >= kmax;
+    }
+    f32x16 sv, dpv;
+    bf16x8 A[2], B[2], pb[2], db[2];
+    f32x4 st[2];  // lse2 / delta quads, loaded two steps before use
+    fetch(0, A[0], B[0]);
+    fetch(1, A[1], B[1]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const int qi = 32 * kk2 + 16 * mb + 4 * g;
-        const f32x4 lse4 = *reinterpret_cast<const f32x4*>(&stat[buf][0][qi]);
-        const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][qi]);
+    for (int j = 0; j < 32; ++j) {
+      const int sl = j & 1;
+      if (j < 8) {
+        sv = mfma32x32x16(A[sl], kreg[j], j == 0 ? f32x16{} : sv);
+      } else if (j < 16) {
+        dpv = mfma32x32x16(A[sl], B[sl], j == 8 ? f32x16{} : dpv);
+      } else if (j < 24) {
+        const int i = j - 16;
+        dv[i & 3] = mfma32x32x16(A[sl], pb[i >> 2], dv[i & 3]);
+      } else {
+        const int i = j - 24;
+        dk[i & 3] = mfma32x32x16(A[sl], db[i >> 2], dk[i & 3]);
+      }
+      if (j + 2 < 32) fetch(j + 2, A[sl], B[sl]);
+      // statistics: lse2 quad w at j = 7 + 2w, delta quad w at j = 16 + 2w
+      if (j >= 7 && j <= 13 && (j & 1)) {
+        const int w = (j - 7) >> 1;
+        st[w & 1] = *reinterpret_cast<const f32x4*>(&lse_[8 * w + 4 * h]);
+      }
+      if (j >= 16 && j <= 22 && !(j & 1)) {
+        const int w = (j - 16) >> 1;
+        st[w & 1] = *reinterpret_cast<const f32x4*>(&dlt_[8 * w + 4 * h]);
+      }
+      // P for elements 2k, 2k+1 at j = 9 + k
+      if (j >= 9 && j <= 16) {
+        const int k = j - 9;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x = s[mb][nb][i];
-            if constexpr (MASKED) {
-              const int kr = 16 * nb + c;
-              const bool bad = (a.causal && kr - (qi + i) > cthr) || kr >= kmax || qi + i >= qmax;
-              x = bad ? -INFINITY : x;
-            }
-            const float p = fast_exp2(fmaf(x, a.sl2, -lse4[i]));
-            s[mb][nb][i] = p;                              // P
-            dp[mb][nb][i] = p * (dp[mb][nb][i] - dl4[i]);  // dS
+        for (int e = 0; e < 2; ++e) {
+          const int v = 2 * k + e, w = v >> 2, r = v & 3;
+          float x = sv[v];
+          if constexpr (MASKED) {
+            // query 4h + (8w + r) against key kc: the per-lane parts are kq, qlim
+            const int qo = 8 * w + r;
+            const bool bad = kbad || (a.causal && kq > cthr + qo) || qo >= qlim;
+            x = bad ? -INFINITY : x;
           }
+          sv[v] = fast_exp2(fmaf(x, a.sl2, -st[w & 1][r]));
         }
       }
-      const bf16x8 p0 = pack_bf16x8(s[0][0], s[1][0]);
-      const bf16x8 p1 = pack_bf16x8(s[0][1], s[1][1]);
-      const bf16x8 d0 = pack_bf16x8(dp[0][0], dp[1][0]);
-      const bf16x8 d1 = pack_bf16x8(dp[0][1], dp[1][1]);
+      // dS for elements 2k, 2k+1 at j = 18 + k
+      if (j >= 18 && j <= 25) {
+        const int k = j - 18;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int off = toff[db] + kk2 * 32 * t128::kRowBytes;
-        const bf16x8 oa = concat_bf16x4(t128::ds_read_tr(ot_ + off),
-                                         t128::ds_read_tr(ot_ + off + 16 * t128::kRowBytes));
-        const bf16x8 qa = concat_bf16x4(t128::ds_read_tr(qt_ + off),
-                                         t128::ds_read_tr(qt_ + off + 16 * t128::kRowBytes));
-        dv[db][0] = mfma16x16x32(oa, p0, dv[db][0]);
-        dv[db][1] = mfma16x16x32(oa, p1, dv[db][1]);
-        dk[db][0] = mfma16x16x32(qa, d0, dk[db][0]);
-        dk[db][1] = mfma16x16x32(qa, d1, dk[db][1]);
+        for (int e = 0; e < 2; ++e) {
+          const int v = 2 * k + e, w = v >> 2, r = v & 3;
+          dpv[v] = sv[v] * (dpv[v] - st[w & 1][r]);
+        }
       }
+      // Packed bf16 B operands (slot 4p + t <- element 8u + 4(t/2) + 2(t%2) + p)
+      if (j == 12 || j == 16) {
+        const int u = (j - 12) >> 2;
+        pb[u] = pack_bf16x8(f32x4{sv[8 * u], sv[8 * u + 2], sv[8 * u + 4], sv[8 * u + 6]},
+                            f32x4{sv[8 * u + 1], sv[8 * u + 3], sv[8 * u + 5], sv[8 * u + 7]});
+      }
+      if (j == 21 || j == 25) {
+        const int u = (j - 21) >> 2;
+        db[u] = pack_bf16x8(f32x4{dpv[8 * u], dpv[8 * u + 2], dpv[8 * u + 4], dpv[8 * u + 6]},
+                            f32x4{dpv[8 * u + 1], dpv[8 * u + 3], dpv[8 * u + 5], dpv[8 * u + 7]});
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -421,19 +481,22 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     }
   }
 
+  // dK^T / dV^T element v of lane l: key kw0 + l%32, dim 32*dblk + 8(v/4) + 4h + v%4.
+  const int row = kw0 + kc;
+  if (row < a.Nk) {
+    const int64_t off = (((int64_t)b * a.Nk + row) * a.Hkv + hk) * D;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int row = kw0 + 16 * nb + c;
-    if (row < a.Nk) {
-      const int64_t off = (((int64_t)b * a.Nk + row) * a.Hkv + hk) * D + 4 * g;
+    for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        f32x4* pk = reinterpret_cast<f32x4*>(a.dk + off + 16 * db);
-        f32x4* pv = reinterpret_cast<f32x4*>(a.dv + off + 16 * db);
-        *pk = *pk + dk[db][nb] * a.scale;
-        *pv = *pv + dv[db][nb];
+      for (int w = 0; w < 4; ++w) {
+        const int d0 = 32 * dblk + 8 * w + 4 * h;
+        f32x4* pk = reinterpret_cast<f32x4*>(a.dk + off + d0);
+        f32x4* pv = reinterpret_cast<f32x4*>(a.dv + off + d0);
+        const f32x4 k4 = {dk[dblk][4 * w], dk[dblk][4 * w + 1], dk[dblk][4 * w + 2], dk[dblk][4 * w + 3]};
+        const f32x4 v4 = {dv[dblk][4 * w], dv[dblk][4 * w + 1], dv[dblk][4 * w + 2], dv[dblk][4 * w + 3]};
+        *pk = *pk + k4 * a.scale;
+        *pv = *pv + v4;
       }
-    }
   }
 }
 

@@ -93,8 +93,8 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   t128::RowLoader<BN, kWaves> ld;
   ld.init(ks, wave, lane);
   if (ntiles > 0) {
-    ld.load(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
-    ld.load(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+    ld.load<true>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
+    ld.load<true>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
   }
 
   // Q^T operand: lane holds query 16*nb + c, head dims 32*kk + 8g .. +7.
@@ -205,8 +205,8 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
     __syncthreads();
     if (j + 1 < ntiles) {
       const int nbuf = (j + 1) & 1;
-      ld.load(kbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][0], wave, lane);
-      ld.load(vbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][1], wave, lane);
+      ld.load<true>(kbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][0], wave, lane);
+      ld.load<true>(vbase, ks, (j + 1) * BN, a.Nk, smem[nbuf][1], wave, lane);
     }
     const int key0 = j * BN;
     const int64_t kp_first = a.k_pos0 + key0;

@@ -43,6 +43,54 @@ __device__ __forceinline__ int swz(int r) {
   return (((r + 4 * (r >> 3)) & 7) << 1) | (r >> 3);
 }
 
+// LDS DMA: each lane copies 16 (dma_b128) or 4 (dma_b32) bytes from global
+// memory to LDS address lds + 16 * lane (4 * lane); lds must be uniform.
+// Issued from inline asm so that the compiler's wait insertion does not track
+// it: it cannot tell which LDS buffer a DMA writes, and would put an
+// s_waitcnt vmcnt(0) before every later LDS read, i.e. wait for a prefetch of
+// the next tile before reading the current one.  Callers wait explicitly
+// (wait_vmem, plus a barrier when several waves fill one tile) before reading
+// the destination.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)p);
+}
+
+// The LDS address goes to M0 through the "{m0}" operand (the compiler then
+// knows M0's value).  The compiler does not insert wait states for the
+// instructions inside an asm statement, so s_nop 4 provides them: 5 for a
+// VALU write of an SGPR (v_readfirstlane of the base or of M0) followed by a
+// VMEM read of it, which also covers the 1 of an M0 write before an LDS DMA.
+__device__ __forceinline__ void dma_b128(const void* g, const void* lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "{m0}"(lds_addr(lds))
+               : "memory");
+}
+
+// A pointer the caller guarantees to be wave-uniform, as SGPRs (an "s" asm
+// operand would otherwise receive a VGPR when uniformity is not provable).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Same, from a uniform base plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void dma_b128(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_addr(lds))
+               : "memory");
+}
+
+__device__ __forceinline__ void dma_b32(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_addr(lds))
+               : "memory");
+}
+
 // Direct global->LDS loader for tiles of ROWS rows of a [*, 128] bf16
 // matrix (row stride `stride` elements), NW waves, one wave instruction per
 // 4 rows.  The per-lane byte offsets inside a tile are computed once; a tile
@@ -63,15 +111,22 @@ struct RowLoader {
     }
   }
 
+  // kTracked: issue through the compiler builtin, whose DMA the compiler
+  // tracks (it then waits for the DMA before any later LDS read); otherwise
+  // through the untracked form above, and the caller waits.
+  template <bool kTracked = false>
   __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int row0, int nrows,
                                        uint8_t* lds, int wave, int lane) const {
     if (row0 + ROWS <= nrows) {
       const uint8_t* tb = reinterpret_cast<const uint8_t*>(base + (int64_t)row0 * stride);
 #pragma unroll
-      for (int i = 0; i < kInst; ++i)
-        __builtin_amdgcn_global_load_lds(tb + off[i],
-                                         (lds_void*)(lds + (i * NW + wave) * 4 * kRowBytes), 16,
-                                         0, 0);
+      for (int i = 0; i < kInst; ++i) {
+        uint8_t* dst = lds + (i * NW + wave) * 4 * kRowBytes;
+        if constexpr (kTracked)
+          __builtin_amdgcn_global_load_lds(tb + off[i], (lds_void*)dst, 16, 0, 0);
+        else
+          dma_b128(tb, off[i], dst);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
@@ -81,7 +136,10 @@ struct RowLoader {
         int grow = row0 + r;
         grow = grow < nrows ? grow : nrows - 1;
         const uint16_t* g = base + (int64_t)grow * stride + chunk * 8;
-        __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+        if constexpr (kTracked)
+          __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+        else
+          dma_b128(g, lds + rblk * kRowBytes);
       }
     }
   }
@@ -93,10 +151,13 @@ __device__ __forceinline__ void load_f32x64(const float* base, int i0, int n, fl
                                             int lane) {
   int i = i0 + lane;
   i = i < n ? i : n - 1;
-  __builtin_amdgcn_global_load_lds(base + i, (lds_void*)lds, 4, 0, 0);
+  dma_b32(base, 4u * (uint32_t)i, lds);
 }
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(0) through the builtin, so that the compiler's wait
+// insertion knows every earlier vector memory load has completed here (it does
+// not parse inline asm).  Immediate: vmcnt 0, expcnt 7, lgkmcnt 15.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Byte offset of logical chunk `chunk` of tile row `r`.
 __device__ __forceinline__ int row_chunk_off(int r, int chunk) {
