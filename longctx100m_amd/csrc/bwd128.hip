@@ -1,5 +1,5 @@
 // Recomputation backward of one ring hop for head_dim 128 on bf16 MFMA
-// (gfx950 v_mfma_f32_16x16x32_bf16, fp32 accumulation).
+// (gfx950 v_mfma_f32_32x32x16_bf16, fp32 accumulation).
 //
 // Semantics (rust/longctx100m-model/src/ring_attention.rs:383-409 and
 // :433-454; src/longctx100m/ring_attention.py:338-357, :373-391):
@@ -15,9 +15,9 @@
 //             S^T = K Q^T, dP^T = V dO^T   (A = K, V rows: ds_read_b128)
 //             dQ^T += K^T dS^T             (A = K^T: ds_read_b64_tr_b16)
 //   dkdv128 KV-stationary, 4 waves x 32 keys of one KV head, walking every
-//           query head of the GQA group (group sum in registers).  K^T, V^T
-//           in VGPRs; 64-query tiles of Q, dO, LSE and delta double-buffered
-//           in LDS.
+//           query head of the GQA group (group sum in registers).  K^T in
+//           VGPRs, the workgroup's V rows in LDS; 32-query tiles of Q, dO,
+//           LSE and delta double-buffered in LDS.
 //             S = Q K^T, dP = dO V^T       (A = Q, dO rows)
 //             dV^T += dO^T P, dK^T += Q^T dS  (A = dO^T, Q^T: transposed reads)
 // Tiles are swizzled row-major and filled by direct global->LDS loads
@@ -33,8 +33,6 @@ namespace lc {
 namespace {
 
 constexpr int D = 128;
-constexpr int KS = D / 32;
-constexpr int DB = D / 16;
 
 struct Bwd128Args {
   const uint16_t* q;
@@ -60,14 +58,26 @@ constexpr int kDqBM = 4 * kDqQW;  // queries per workgroup
 constexpr int kDqBN = 64;         // keys per tile
 constexpr int kDqTile = kDqBN * t128::kRowBytes;
 
+// dQ with v_mfma_f32_32x32x16_bf16: each lane holds one query (lane % 32)
+// of the wave's 32, so LSE and delta are one register each.  One 64-key tile
+// is a stream of 48 MFMA steps j with LDS operands fetched two steps ahead:
+//   j  0-15  S^T  = K Q^T      (mb, t) = (j % 2, j / 2)       A = K rows
+//   j 16-31  dP^T = V dO^T     (mb, t) = ((j-16) / 8, (j-16) % 8), A = V rows
+//   j 32-47  dQ^T += K^T dS^T  (u, dblk) = ((j-32) / 4, (j-32) % 4),
+//                              A = K^T (transposed reads of the K tile)
+// with P formed on the VALU during the dP steps and dS = P (dP - delta)
+// during j 25-28 (keys 0-31) and 33-36 (keys 32-63).  The three phases are
+// separate fully unrolled loops (one 48-step loop exceeds the unroller's
+// limit, and a rolled loop would index the score arrays dynamically).  Score element v of
+// block mb: key 32mb + 8(v/4) + 4(lane/32) + v%4.
 __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kDqTile];  // [buf][K,V]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int c = lane & 15;
-  const int g = lane >> 4;
+  const int kc = lane & 31;  // this lane's query within the wave
+  const int hh = lane >> 5;
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = a.n_tiles - 1 - (L % a.n_tiles);
@@ -93,89 +103,114 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
   const int ntiles = kend > 0 ? (int)((kend + kDqBN - 1) / kDqBN) : 0;
   if (ntiles == 0) return;  // nothing visible: dQ gets no contribution
 
+  const uint32_t smem_lds = t128::lds_addr(smem);
   t128::RowLoader<kDqBN, 4> ld;
   ld.init(ks, wave, lane);
-  ld.load<true>(kbase, ks, 0, a.Nk, smem[0][0], wave, lane);
-  ld.load<true>(vbase, ks, 0, a.Nk, smem[0][1], wave, lane);
+  ld.load(kbase, ks, 0, a.Nk, smem_lds, wave, lane);
+  ld.load(vbase, ks, 0, a.Nk, smem_lds + kDqTile, wave, lane);
 
-  bf16x8 qreg[2][KS], doreg[2][KS];
-  float lse[2], dl[2];
+  // Q^T, dO^T as B operands: lane holds query qw0 + kc, dims 16t + 8hh .. +7.
+  bf16x8 qreg[D / 16], doreg[D / 16];
+  float lse, dl;
+  {
+    const int row = min(qw0 + kc, a.Nq - 1);
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int row = min(qw0 + 16 * nb + c, a.Nq - 1);
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      qreg[nb][kk] = *reinterpret_cast<const bf16x8*>(qbase + (int64_t)row * qs + 32 * kk + 8 * g);
-      doreg[nb][kk] = *reinterpret_cast<const bf16x8*>(obase + (int64_t)row * qs + 32 * kk + 8 * g);
+    for (int t = 0; t < D / 16; ++t) {
+      qreg[t] = *reinterpret_cast<const bf16x8*>(qbase + (int64_t)row * qs + 16 * t + 8 * hh);
+      doreg[t] = *reinterpret_cast<const bf16x8*>(obase + (int64_t)row * qs + 16 * t + 8 * hh);
     }
     const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
-    lse[nb] = a.lse2[si];
-    dl[nb] = a.delta[si];
+    lse = a.lse2[si];
+    dl = a.delta[si];
   }
 
-  int roff[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) roff[kk] = t128::row_chunk_off(c, 4 * kk + g);
-  int toff[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) toff[db] = t128::tr_off(0, 16 * db, lane);
+  const int roff0 = t128::row_chunk_off(kc, hh);  // row 32mb + kc, dims 16t + 8hh: ^ (32 t)
+  const int toff0 = t128::tr32_off(0, lane), toff1 = t128::tr32_off(1, lane);
 
   const int64_t wq_first = a.q_pos0 + qw0;
   const int64_t wq_last = wq_first + kDqQW - 1;
 
-  f32x4 acc[DB][2];
+  f32x16 acc[4];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
 
-  // One tile, per 32-key half (kk2): S^T = K Q^T and dP^T = V dO^T for keys
-  // 32*kk2 + [16mb+4g+i] x query 16nb+c, then dQ^T += K^T dS^T.  Mask (MASKED
-  // only): key k of the tile / query q of the wave are invalid when
-  // (causal && k - q > cthr) || k >= kmax.
+  // Mask (MASKED only): key idx + 4hh of the tile and query kc are invalid
+  // when (causal && idx + 4hh - kc > cthr) || idx + 4hh >= kmax.
   auto tile = [&](auto masked_tag, const uint8_t* kt, const uint8_t* vt, int cthr, int kmax) {
     constexpr bool MASKED = decltype(masked_tag)::value;
+    const int ro = opaque(roff0);
+    const int to0 = opaque(toff0), to1 = opaque(toff1);
+    int kq = 0, klim = 0;
+    if constexpr (MASKED) {
+      kq = opaque(4 * hh - kc);
+      klim = opaque(kmax - 4 * hh);
+    }
+    auto fetch = [&](int j) {
+      if (j < 16) {
+        return *reinterpret_cast<const bf16x8*>(kt + ((ro ^ (32 * (j >> 1))) + (j & 1) * 32 * t128::kRowBytes));
+      } else if (j < 32) {
+        const int i = j - 16;
+        return *reinterpret_cast<const bf16x8*>(vt + ((ro ^ (32 * (i & 7))) + (i >> 3) * 32 * t128::kRowBytes));
+      } else {
+        const int i = j - 32;
+        const int o0 = (to0 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+        const int o1 = (to1 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+        return concat_bf16x4(t128::ds_read_tr(kt + o0), t128::ds_read_tr(kt + o1));
+      }
+    };
+    f32x16 sv[2], dpv[2];
+    bf16x8 A[2], dsb[4];
+    // P for scores 4k .. 4k+3 (k = 0..7)
+    auto probs = [&](int k) {
 #pragma unroll
-    for (int kk2 = 0; kk2 < kDqBN / 32; ++kk2) {
-      f32x4 s[2][2], dp[2][2];
+      for (int e = 4 * k; e < 4 * k + 4; ++e) {
+        const int mb = e >> 4, v = e & 15;
+        float x = sv[mb][v];
+        if constexpr (MASKED) {
+          const int idx = 32 * mb + 8 * (v >> 2) + (v & 3);
+          const bool bad = (a.causal && kq > cthr - idx) || idx >= klim;
+          x = bad ? -INFINITY : x;
+        }
+        sv[mb][v] = fast_exp2(fmaf(x, a.sl2, -lse));
+      }
+    };
+    // dS for scores 4k .. 4k+3 of block mb (k = 0..3); packed at k = 3
+    auto dscore = [&](int mb, int k) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        s[mb][0] = s[mb][1] = dp[mb][0] = dp[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int e = 4 * k; e < 4 * k + 4; ++e) dpv[mb][e] = sv[mb][e] * (dpv[mb][e] - dl);
+      if (k == 3) {
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const int off = roff[kk] + (2 * kk2 + mb) * 16 * t128::kRowBytes;
-          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kt + off);
-          const bf16x8 va = *reinterpret_cast<const bf16x8*>(vt + off);
-          s[mb][0] = mfma16x16x32(ka, qreg[0][kk], s[mb][0]);
-          s[mb][1] = mfma16x16x32(ka, qreg[1][kk], s[mb][1]);
-          dp[mb][0] = mfma16x16x32(va, doreg[0][kk], dp[mb][0]);
-          dp[mb][1] = mfma16x16x32(va, doreg[1][kk], dp[mb][1]);
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const int e0 = 8 * u2;
+          dsb[2 * mb + u2] = pack_bf16x8(
+              f32x4{dpv[mb][e0], dpv[mb][e0 + 2], dpv[mb][e0 + 4], dpv[mb][e0 + 6]},
+              f32x4{dpv[mb][e0 + 1], dpv[mb][e0 + 3], dpv[mb][e0 + 5], dpv[mb][e0 + 7]});
         }
       }
+    };
+    A[0] = fetch(0);
+    A[1] = fetch(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+    for (int j = 0; j < 16; ++j) {  // S^T
+      sv[j & 1] = mfma32x32x16(A[j & 1], qreg[j >> 1], j < 2 ? f32x16{} : sv[j & 1]);
+      A[j & 1] = fetch(j + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+    for (int i = 0; i < 16; ++i) {  // dP^T, P, dS of keys 0-31
+      dpv[i >> 3] = mfma32x32x16(A[i & 1], doreg[i & 7], (i & 7) == 0 ? f32x16{} : dpv[i >> 3]);
+      A[i & 1] = fetch(16 + i + 2);
+      if (i >= 1 && i <= 8) probs(i - 1);
+      if (i >= 9 && i <= 12) dscore(0, i - 9);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x = s[mb][nb][i];
-            if constexpr (MASKED) {
-              const int kr = 32 * kk2 + 16 * mb + 4 * g + i;
-              const bool bad = (a.causal && kr - (16 * nb + c) > cthr) || kr >= kmax;
-              x = bad ? -INFINITY : x;
-            }
-            const float p = fast_exp2(fmaf(x, a.sl2, -lse[nb]));
-            s[mb][nb][i] = p * (dp[mb][nb][i] - dl[nb]);  // dS^T
-          }
-      const bf16x8 b0 = pack_bf16x8(s[0][0], s[1][0]);
-      const bf16x8 b1 = pack_bf16x8(s[0][1], s[1][1]);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint8_t* p = kt + toff[db] + kk2 * 32 * t128::kRowBytes;
-        const bf16x8 ka = concat_bf16x4(t128::ds_read_tr(p), t128::ds_read_tr(p + 16 * t128::kRowBytes));
-        acc[db][0] = mfma16x16x32(ka, b0, acc[db][0]);
-        acc[db][1] = mfma16x16x32(ka, b1, acc[db][1]);
-      }
+    for (int i = 0; i < 16; ++i) {  // dQ^T, dS of keys 32-63
+      acc[i & 3] = mfma32x32x16(A[i & 1], dsb[i >> 2], acc[i & 3]);
+      if (i + 2 < 16) A[i & 1] = fetch(32 + i + 2);
+      if (i >= 1 && i <= 4) dscore(1, i - 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -183,9 +218,9 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
     t128::wait_vmem();
     __syncthreads();
     if (j + 1 < ntiles) {
-      const int nbuf = (j + 1) & 1;
-      ld.load<true>(kbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][0], wave, lane);
-      ld.load<true>(vbase, ks, (j + 1) * kDqBN, a.Nk, smem[nbuf][1], wave, lane);
+      const uint32_t nb = smem_lds + ((j + 1) & 1) * 2 * kDqTile;
+      ld.load(kbase, ks, (j + 1) * kDqBN, a.Nk, nb, wave, lane);
+      ld.load(vbase, ks, (j + 1) * kDqBN, a.Nk, nb + kDqTile, wave, lane);
     }
     const int key0 = j * kDqBN;
     const int64_t kp_first = a.k_pos0 + key0;
@@ -205,17 +240,18 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
     }
   }
 
+  // dQ^T element v of lane l: query qw0 + kc, dim 32*dblk + 8(v/4) + 4hh + v%4.
+  const int row = qw0 + kc;
+  if (row < a.Nq) {
+    float* dst = a.dq + (((int64_t)b * a.Nq + row) * a.Hq + h) * D;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int row = qw0 + 16 * nb + c;
-    if (row < a.Nq) {
-      float* dst = a.dq + (((int64_t)b * a.Nq + row) * a.Hq + h) * D + 4 * g;
+    for (int d = 0; d < 4; ++d)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        f32x4* p = reinterpret_cast<f32x4*>(dst + 16 * db);
-        *p = *p + acc[db][nb] * a.scale;
+      for (int w = 0; w < 4; ++w) {
+        f32x4* p = reinterpret_cast<f32x4*>(dst + 32 * d + 8 * w + 4 * hh);
+        const f32x4 v4 = {acc[d][4 * w], acc[d][4 * w + 1], acc[d][4 * w + 2], acc[d][4 * w + 3]};
+        *p = *p + v4 * a.scale;
       }
-    }
   }
 }
 
@@ -225,34 +261,6 @@ constexpr int kKvKW = 32;
 constexpr int kKvBN = 4 * kKvKW;  // keys per workgroup
 constexpr int kKvBM = 32;         // queries per tile
 constexpr int kKvTile = kKvBM * t128::kRowBytes;
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Byte offset of a transposed read for the 32x32x16 A operand X^T (X = a
-// [32 x 128] Q or dO tile; k index = query row, m index = column), column
-// block 0 and k-half p: lane l receives X[row(l/32, p, t)][l%32] in slot t,
-// with row(h, p, t) = 4h + p + 2(t%2) + 8(t/2).  The four rows read in one
-// cycle (lanes 0-31 or 32-63) then have distinct swz(r) / 4, so the 4 rows x
-// 4 chunks land on 16 distinct chunks (no bank conflict).  Column block dblk
-// is offset ^ (64 * dblk) (the block index occupies chunk bits 2-3 alone);
-// rows 16 .. 31 are offset + 16 * kRowBytes (swz depends on r % 16).
-__device__ __forceinline__ int tr32_off(int p, int lane) {
-  const int G = lane >> 4, i = lane & 15, t = i >> 2;
-  const int col = 16 * (G & 1) + 4 * (i & 3);
-  const int r = 4 * (G >> 1) + p + 2 * (t & 1) + 8 * (t >> 1);
-  return r * t128::kRowBytes + 16 * ((col >> 3) ^ t128::swz(r)) + 2 * (col & 7);
-}
-
-// Hides a value from loop-invariant code motion, so offsets derived from it
-// by an XOR are formed next to their use instead of occupying registers.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
 
 // dK/dV with v_mfma_f32_32x32x16_bf16: one 32x32 score block per wave and
 // query tile, so half the MFMA instructions of the 16x16x32 form.
@@ -306,11 +314,11 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   auto issue = [&](int hq, int qrow0, int buf) {
     const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
     const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
-    ld.load(qb, qs, qrow0, a.Nq, smem[buf][0], wave, lane);
-    ld.load(ob, qs, qrow0, a.Nq, smem[buf][1], wave, lane);
+    ld.load(qb, qs, qrow0, a.Nq, t128::lds_addr(smem) + buf * 2 * kKvTile, wave, lane);
+    ld.load(ob, qs, qrow0, a.Nq, t128::lds_addr(smem) + (buf * 2 + 1) * kKvTile, wave, lane);
     const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.Nq;
-    if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, stat[buf][0], lane);
-    if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, stat[buf][1], lane);
+    if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, t128::lds_addr(stat) + buf * 512, lane);
+    if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, t128::lds_addr(stat) + buf * 512 + 256, lane);
   };
   const int hq0 = hk * a.group;
   issue(hq0, qstart, 0);
@@ -326,14 +334,14 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   {
     t128::RowLoader<kKvBN, 4> vld;
     vld.init(ks, wave, lane);
-    vld.load(vbase, ks, k0, a.Nk, v_lds, wave, lane);
+    vld.load(vbase, ks, k0, a.Nk, t128::lds_addr(v_lds), wave, lane);
   }
 
   // Row l%32 of a Q/dO tile, dims 16t + 8h .. +7, is roff0 ^ (32 t); the
   // wave's V rows are the same offsets in the wave's part of the V tile.
   const int roff0 = t128::row_chunk_off(kc, h);
   const int voff0 = roff0 + wave * kKvKW * t128::kRowBytes;
-  const int toff0 = tr32_off(0, lane), toff1 = tr32_off(1, lane);
+  const int toff0 = t128::tr32_off(0, lane), toff1 = t128::tr32_off(1, lane);
   f32x16 dk[4], dv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) dk[i] = dv[i] = f32x16{};

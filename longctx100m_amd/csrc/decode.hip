@@ -70,8 +70,8 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   t128::RowLoader<TK, 1> ld;
   ld.init(ks, 0, lane);
   if (ntiles > 0) {
-    ld.load(kbase, ks, (int)kb0, a.Nk, kbuf[0], 0, lane);
-    ld.load(vbase, ks, (int)kb0, a.Nk, vbuf[0], 0, lane);
+    ld.load(kbase, ks, (int)kb0, a.Nk, t128::lds_addr(kbuf), 0, lane);
+    ld.load(vbase, ks, (int)kb0, a.Nk, t128::lds_addr(vbuf), 0, lane);
   }
 
   // Row c of this (batch, KV head): query head hk*group + c / Nq, query c % Nq.
@@ -105,8 +105,8 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   for (int j = 0; j < ntiles; ++j) {
     t128::wait_vmem();
     if (j + 1 < ntiles) {
-      ld.load(kbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, kbuf[(j + 1) & 1], 0, lane);
-      ld.load(vbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, vbuf[(j + 1) & 1], 0, lane);
+      ld.load(kbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, t128::lds_addr(kbuf) + ((j + 1) & 1) * kTileBytes, 0, lane);
+      ld.load(vbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, t128::lds_addr(vbuf) + ((j + 1) & 1) * kTileBytes, 0, lane);
     }
     const uint8_t* kt = kbuf[j & 1];
     const uint8_t* vt = vbuf[j & 1];

@@ -51,20 +51,11 @@ __device__ __forceinline__ int swz(int r) {
 // the next tile before reading the current one.  Callers wait explicitly
 // (wait_vmem, plus a barrier when several waves fill one tile) before reading
 // the destination.
+// LDS byte address of a pointer into a __shared__ array (pass the array
+// itself or a constant offset into it, so that the cast folds to a constant;
+// tiles are then addressed as that constant plus an offset).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)p);
-}
-
-// The LDS address goes to M0 through the "{m0}" operand (the compiler then
-// knows M0's value).  The compiler does not insert wait states for the
-// instructions inside an asm statement, so s_nop 4 provides them: 5 for a
-// VALU write of an SGPR (v_readfirstlane of the base or of M0) followed by a
-// VMEM read of it, which also covers the 1 of an M0 write before an LDS DMA.
-__device__ __forceinline__ void dma_b128(const void* g, const void* lds) {
-  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "{m0}"(lds_addr(lds))
-               : "memory");
+  return (uint32_t)(uintptr_t)(lds_void*)p;
 }
 
 // A pointer the caller guarantees to be wave-uniform, as SGPRs (an "s" asm
@@ -76,32 +67,45 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Same, from a uniform base plus a per-lane 32-bit byte offset.
-__device__ __forceinline__ void dma_b128(const void* base, uint32_t off, const void* lds) {
-  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+// The LDS address (uniform) goes to M0 through the "{m0}" operand, so the
+// compiler knows M0's value.  The compiler does not insert wait states for
+// the instructions inside an asm statement, so s_nop 4 provides them: 5 for a
+// VALU write of an SGPR (v_readfirstlane of the base or of M0) followed by a
+// VMEM read of it, which also covers the 1 of an M0 write before an LDS DMA.
+__device__ __forceinline__ void dma_b128(const void* g, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off"
                :
-               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_addr(lds))
+               : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 
-__device__ __forceinline__ void dma_b32(const void* base, uint32_t off, const void* lds) {
+// Same, from a uniform base plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void dma_b128(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
+__device__ __forceinline__ void dma_b32(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
                :
-               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_addr(lds))
+               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 
 // Direct global->LDS loader for tiles of ROWS rows of a [*, 128] bf16
 // matrix (row stride `stride` elements), NW waves, one wave instruction per
-// 4 rows.  The per-lane byte offsets inside a tile are computed once; a tile
-// that lies fully inside the matrix is issued from a uniform base pointer
-// plus those offsets, the last (partial) tile re-reads row nrows - 1 for
-// rows past the end (finite data; callers mask those rows).
+// 4 rows.  The per-lane byte offsets inside a tile and the wave's LDS offset
+// are computed once; a tile that lies fully inside the matrix is issued from
+// a uniform base pointer plus those offsets, the last (partial) tile re-reads
+// row nrows - 1 for rows past the end (finite data; callers mask those rows).
 template <int ROWS, int NW>
 struct RowLoader {
   static_assert(ROWS % (4 * NW) == 0, "4 rows per wave instruction");
   static constexpr int kInst = ROWS / (4 * NW);
   uint32_t off[kInst];  // byte offset of this lane's 16-byte chunk within a tile
+  uint32_t wave_lds;    // LDS byte offset of this wave's first 4 rows (uniform)
 
   __device__ __forceinline__ void init(int64_t stride, int wave, int lane) {
 #pragma unroll
@@ -109,45 +113,47 @@ struct RowLoader {
       const int r = (i * NW + wave) * 4 + (lane >> 4);
       off[i] = (uint32_t)(r * stride * 2 + 16 * ((lane & 15) ^ swz(r)));
     }
+    wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)wave * 4 * kRowBytes);
   }
 
-  // kTracked: issue through the compiler builtin, whose DMA the compiler
-  // tracks (it then waits for the DMA before any later LDS read); otherwise
-  // through the untracked form above, and the caller waits.
+  // lds: LDS byte address of the tile.  kTracked: issue through the compiler
+  // builtin, whose DMA the compiler tracks (it then waits for the DMA before
+  // any later LDS read); otherwise through the untracked form above, and the
+  // caller waits.
   template <bool kTracked = false>
   __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int row0, int nrows,
-                                       uint8_t* lds, int wave, int lane) const {
+                                       uint32_t lds, int wave, int lane) const {
     if (row0 + ROWS <= nrows) {
       const uint8_t* tb = reinterpret_cast<const uint8_t*>(base + (int64_t)row0 * stride);
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
-        uint8_t* dst = lds + (i * NW + wave) * 4 * kRowBytes;
+        const uint32_t dst = lds + wave_lds + i * NW * 4 * kRowBytes;
         if constexpr (kTracked)
-          __builtin_amdgcn_global_load_lds(tb + off[i], (lds_void*)dst, 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(tb + off[i], (lds_void*)(uintptr_t)dst, 16, 0, 0);
         else
           dma_b128(tb, off[i], dst);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
-        const int rblk = (i * NW + wave) * 4;
-        const int r = rblk + (lane >> 4);
+        const int r = (i * NW + wave) * 4 + (lane >> 4);
         const int chunk = (lane & 15) ^ swz(r);
         int grow = row0 + r;
         grow = grow < nrows ? grow : nrows - 1;
         const uint16_t* g = base + (int64_t)grow * stride + chunk * 8;
+        const uint32_t dst = lds + wave_lds + i * NW * 4 * kRowBytes;
         if constexpr (kTracked)
-          __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + rblk * kRowBytes), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(g, (lds_void*)(uintptr_t)dst, 16, 0, 0);
         else
-          dma_b128(g, lds + rblk * kRowBytes);
+          dma_b128(g, dst);
       }
     }
   }
 };
 
-// Direct load of 64 consecutive fp32 values (one wave instruction).
-// Entries at or beyond n re-read entry n - 1.
-__device__ __forceinline__ void load_f32x64(const float* base, int i0, int n, float* lds,
+// Direct load of 64 consecutive fp32 values (one wave instruction) to LDS
+// byte address lds.  Entries at or beyond n re-read entry n - 1.
+__device__ __forceinline__ void load_f32x64(const float* base, int i0, int n, uint32_t lds,
                                             int lane) {
   int i = i0 + lane;
   i = i < n ? i : n - 1;
@@ -173,6 +179,24 @@ __device__ __forceinline__ int tr_off(int row0, int col0, int lane) {
   const int r = row0 + 4 * g + (i >> 2);
   const int q = i & 3;
   const int col = col0 + 4 * q;
+  return r * kRowBytes + 16 * ((col >> 3) ^ swz(r)) + 2 * (col & 7);
+}
+
+// Byte offset of a transposed read for the 32x32x16 A operand X^T (X a tile
+// of this file; k index = tile row, m index = column), column block 0 and
+// k-half p: lane l receives X[row(l/32, p, t)][l%32] in slot t, with
+// row(h, p, t) = 4h + p + 2(t%2) + 8(t/2).  The four rows read in one cycle
+// (lanes 0-31 or 32-63) then have distinct swz(r) / 4, so the 4 rows x 4
+// chunks land on 16 distinct chunks (no bank conflict).  Column block dblk is
+// offset ^ (64 * dblk) (the block index occupies chunk bits 2-3 alone); rows
+// 16u .. 16u+15 are offset + 16u * kRowBytes (swz depends on r % 16).  A B
+// operand built from 32x32 accumulators over the same rows must use the same
+// order: k-step u, slot 4p + t <- element 8u' + 4(t/2) + 2(t%2) + p of the
+// block holding rows 16u .. 16u+15 (u' = u % 2).
+__device__ __forceinline__ int tr32_off(int p, int lane) {
+  const int G = lane >> 4, i = lane & 15, t = i >> 2;
+  const int col = 16 * (G & 1) + 4 * (i & 3);
+  const int r = 4 * (G >> 1) + p + 2 * (t & 1) + 8 * (t >> 1);
   return r * kRowBytes + 16 * ((col >> 3) ^ swz(r)) + 2 * (col & 7);
 }
 
