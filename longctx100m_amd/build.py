@@ -5,13 +5,18 @@
 Every translation unit under csrc/ is compiled to an object in _build/ and
 linked into lib/liblongctx100m_attn.so, in-tree, so the library travels with
 the source tree.  All HIP code is compiled with packed-fp32 instructions
-disabled.
+disabled.  The compiler's per-kernel resource report (registers, scratch,
+occupancy, LDS) is written to _build/resource_usage.txt, and the build fails
+when a hot kernel uses more scratch memory per lane than SCRATCH_LIMITS
+allows (a register array indexed at run time, or a spill inside a hot loop,
+costs far more than any tuning gains).
 """
 
 from __future__ import annotations
 
 import argparse
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -44,6 +49,36 @@ EXTRA_FLAGS = {
 }
 
 
+# Kernel (mangled-name substring) -> allowed scratch bytes per lane.  The
+# dK/dV kernel keeps a few loop-invariant mask values in scratch, reloaded only
+# on tiles that need the mask.
+SCRATCH_LIMITS = {
+    "fwd128_kernel": 0,
+    "dq128_kernel": 0,
+    "dkdv128_kernel": 64,
+    "decode128_kernel": 0,
+}
+
+# "Function Name: <kernel>" starts a kernel's block; then "<field> [unit]: value".
+_REMARK = re.compile(r"remark:\s+(?:Function Name: (\S+)|(\w[\w ]*?)(?: \[[^\]]*\])?: (\S+)) \[-Rpass")
+
+
+def _resource_usage(stderr: str) -> dict[str, dict[str, str]]:
+    """Parses -Rpass-analysis=kernel-resource-usage remarks: kernel -> {field: value}."""
+    out: dict[str, dict[str, str]] = {}
+    cur = None
+    for line in stderr.splitlines():
+        m = _REMARK.search(line)
+        if not m:
+            continue
+        if m.group(1):
+            cur = m.group(1)
+            out[cur] = {}
+        elif cur is not None:
+            out[cur][m.group(2).strip()] = m.group(3)
+    return out
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -51,13 +86,34 @@ def hipcc() -> str:
     return exe
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path) -> tuple[Path, dict[str, dict[str, str]]]:
     obj = BUILD / (src.name + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    remarks = ["-Rpass-analysis=kernel-resource-usage"] if src.suffix == ".hip" else []
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), *remarks, "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    return obj
+    return obj, _resource_usage(res.stderr)
+
+
+def _check_resources(usage: dict[str, dict[str, str]]) -> None:
+    lines = []
+    for name in sorted(usage):
+        f = usage[name]
+        lines.append(f"{name}: VGPRs {f.get('VGPRs')} AGPRs {f.get('AGPRs')} "
+                     f"scratch {f.get('ScratchSize')} B/lane occupancy {f.get('Occupancy')} "
+                     f"waves/SIMD LDS {f.get('LDS Size')} B")
+    (BUILD / "resource_usage.txt").write_text("\n".join(lines) + "\n")
+    for key, limit in SCRATCH_LIMITS.items():
+        hits = [n for n in usage if key in n]
+        if not hits:
+            raise RuntimeError(f"resource report has no kernel matching {key!r}")
+        for n in hits:
+            scratch = int(usage[n].get("ScratchSize", "0"))
+            if scratch > limit:
+                raise RuntimeError(f"{n} uses {scratch} bytes/lane of scratch (limit {limit}); "
+                                   "see _build/resource_usage.txt")
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
@@ -67,7 +123,12 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     sources = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
     jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
+        results = list(ex.map(_compile, sources))
+    objs = [obj for obj, _ in results]
+    usage: dict[str, dict[str, str]] = {}
+    for _, u in results:
+        usage.update(u)
+    _check_resources(usage)
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
