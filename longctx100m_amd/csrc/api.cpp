@@ -8,6 +8,7 @@
 // caller binds.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -103,14 +104,40 @@ bool pair_active(const lc::Problem& p) {
   return lc::key_end_for(p, p.Nq) > 0;
 }
 
+// Keys per launch of the d=128 forward.  Every workgroup of a head streams
+// the same K/V tiles, and L2 serves them to the workgroups of an XCD only
+// while those stay within a few hundred tiles of each other; over a longer
+// key range they drift apart and the tiles come from HBM again (measured at
+// 1M keys: 16x the memory traffic).  A longer shard therefore runs as
+// sub-shards of this many keys, each LSE-merged into the running (o, m, l) by
+// the kernel's epilogue, as the ring merges its hops.
+constexpr int64_t kFwdKvChunk = 65536;
+
 int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v, float* o,
               float* m, float* l, hipStream_t st) {
-  hipError_t e;
-  if (use_mfma(p, q, k, v, nullptr))
-    e = p.D == 128 ? lc::launch_fwd128(p, q, k, v, o, m, l, st)
-                   : lc::launch_fwd_mfma(p, q, k, v, o, m, l, st);
-  else
+  hipError_t e = hipSuccess;
+  if (use_mfma(p, q, k, v, nullptr) && p.D == 128) {
+    if (p.Nk <= kFwdKvChunk) {
+      e = lc::launch_fwd128(p, q, k, v, o, m, l, st);
+    } else {
+      const size_t row_bytes = (size_t)p.Hkv * p.D * 2;  // bf16 K/V row
+      bool first = true;
+      for (int64_t c0 = 0; c0 < p.Nk && e == hipSuccess; c0 += kFwdKvChunk) {
+        lc::Problem pc = p;
+        pc.Nk = (int)std::min<int64_t>(kFwdKvChunk, p.Nk - c0);
+        pc.k_pos0 = p.k_pos0 + c0;
+        if (!pair_active(pc)) continue;  // the running state is unchanged
+        const char* kc = static_cast<const char*>(k) + c0 * row_bytes;
+        const char* vc = static_cast<const char*>(v) + c0 * row_bytes;
+        e = lc::launch_fwd128(pc, q, kc, vc, o, m, l, st, p.Nk, !first);
+        first = false;
+      }
+    }
+  } else if (use_mfma(p, q, k, v, nullptr)) {
+    e = lc::launch_fwd_mfma(p, q, k, v, o, m, l, st);
+  } else {
     e = lc::launch_fwd_generic(p, q, k, v, o, m, l, st);
+  }
   if (e != hipSuccess) return hip_error(e, "lc_attn_fwd_shard launch");
   return LC_OK;
 }

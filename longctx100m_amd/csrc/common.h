@@ -118,6 +118,30 @@ __device__ __forceinline__ float xor16_sum(float x) {
 __device__ __forceinline__ float group4_max(float x) { return xor16_max(xor32_max(x)); }
 __device__ __forceinline__ float group4_sum(float x) { return xor16_sum(xor32_sum(x)); }
 
+// Weights of the two partials in the merged output.  With m = max(m_a, m_b):
+// l = e^{m_a-m} l_a + e^{m_b-m} l_b and o = (e^{m_a-m} l_a o_a + e^{m_b-m} l_b o_b) / l,
+// which equals carrying the reference's unnormalised (m, l, acc) across the
+// two partials (rs:36-53 applied blockwise).  No key seen on either side:
+// weights 0, l = 0, m = -inf.
+struct MergeW {
+  float wa, wb, m, l;
+};
+__device__ __forceinline__ MergeW merge_weights(float ma, float la, float mb, float lb) {
+  MergeW w;
+  w.m = fmaxf(ma, mb);
+  if (w.m == -INFINITY) {
+    w.wa = w.wb = w.l = 0.f;
+    return w;
+  }
+  const float ea = expf(ma - w.m) * la;
+  const float eb = expf(mb - w.m) * lb;
+  w.l = ea + eb;
+  const float inv = w.l > 0.f ? 1.f / w.l : 0.f;
+  w.wa = ea * inv;
+  w.wb = eb * inv;
+  return w;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup p runs on
 // XCD p % 8).  Give every XCD a contiguous range of logical tile ids so the
 // tiles that share K/V (same head) share that XCD's L2.

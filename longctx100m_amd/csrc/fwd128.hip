@@ -60,8 +60,10 @@ struct Fwd128Args {
   float* l;
   int Nq, Nk, Hq, Hkv, group, n_qtiles;
   int64_t q_pos0, k_pos0, valid;
+  int64_t kv_bstride;  // elements between batches of K and V
   int causal;
-  float sl2;  // scale * log2(e)
+  int accumulate;  // merge into the running (o, m, l) instead of writing them
+  float sl2;       // scale * log2(e)
 };
 
 __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
@@ -84,8 +86,8 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   const int64_t qs = (int64_t)a.Hq * D;
   const int64_t ks = (int64_t)a.Hkv * D;
   const uint16_t* qbase = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
-  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
-  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.kv_bstride + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.kv_bstride + (int64_t)hk * D;
 
   const int q0 = qt * BM;
   const int qw0 = q0 + wave * kQW;
@@ -282,23 +284,34 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   }
 
   // Epilogue: o = acc / l; m in natural-log units; l as the reference defines it.
+  // accumulate: LSE-merge (o, m, l) into the running state of the row.
   const float lt = xor32_sum(lsum);  // relative to mrun
   const int row = qw0 + kc;
   if (row < a.Nq) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const float ltrue = lt > 0.f ? lt * fast_exp2(mrun - mtrue) : 0.f;
+    const float mnat = (mtrue == -INFINITY) ? -INFINITY : mtrue * kLn2;
     float* orow = a.o + (((int64_t)b * a.Nq + row) * a.Hq + hq) * D;
+    const int64_t si = ((int64_t)b * a.Hq + hq) * a.Nq + row;
+    float wa = 0.f, wb = inv, mo = mnat, lo = ltrue;
+    if (a.accumulate) {
+      const MergeW w = merge_weights(a.m[si], a.l[si], mnat, ltrue);
+      wa = w.wa;
+      wb = w.wb * inv;
+      mo = w.m;
+      lo = w.l;
+    }
 #pragma unroll
     for (int d = 0; d < 4; ++d)
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
+        f32x4* dst = reinterpret_cast<f32x4*>(orow + 32 * d + 8 * w + 4 * hh);
         const f32x4 v4 = {o[d][4 * w], o[d][4 * w + 1], o[d][4 * w + 2], o[d][4 * w + 3]};
-        *reinterpret_cast<f32x4*>(orow + 32 * d + 8 * w + 4 * hh) = v4 * inv;
+        *dst = a.accumulate ? *dst * wa + v4 * wb : v4 * wb;
       }
     if (hh == 0) {
-      const int64_t si = ((int64_t)b * a.Hq + hq) * a.Nq + row;
-      a.m[si] = (mtrue == -INFINITY) ? -INFINITY : mtrue * kLn2;
-      a.l[si] = ltrue;
+      a.m[si] = mo;
+      a.l[si] = lo;
     }
   }
 }
@@ -306,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
 }  // namespace
 
 hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const void* v, float* o,
-                         float* m, float* l, hipStream_t s) {
+                         float* m, float* l, hipStream_t s, int64_t kv_rows, bool accumulate) {
   if (p.D != D) return hipErrorInvalidValue;
   Fwd128Args a;
   a.q = static_cast<const uint16_t*>(q);
@@ -324,7 +337,9 @@ hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const v
   a.q_pos0 = p.q_pos0;
   a.k_pos0 = p.k_pos0;
   a.valid = p.valid;
+  a.kv_bstride = (kv_rows < 0 ? p.Nk : kv_rows) * (int64_t)p.Hkv * D;
   a.causal = p.causal ? 1 : 0;
+  a.accumulate = accumulate ? 1 : 0;
   a.sl2 = p.scale * kLog2e;
   hipLaunchKernelGGL(fwd128_kernel, dim3(a.n_qtiles * p.Hq * p.B), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -34,8 +34,14 @@ inline int64_t key_end_for(const Problem& p, int64_t q_end) {
 bool mfma_supported(const Problem& p);
 
 // head_dim 128: swizzled direct-to-LDS tiles (fwd128.hip, bwd128.hip).
+// The forward can run on a sub-shard of the keys: k and v point at its first
+// key, p.Nk and p.k_pos0 describe the sub-shard, kv_rows is the key count of
+// the whole shard (the batch stride of K and V; -1: p.Nk), and accumulate
+// merges the result into the running (o, m, l) with the weights of
+// lc_attn_merge instead of overwriting them.
 hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const void* v, float* o,
-                         float* m, float* l, hipStream_t s);
+                         float* m, float* l, hipStream_t s, int64_t kv_rows = -1,
+                         bool accumulate = false);
 hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const void* v,
                         const void* dout, const float* lse2, const float* delta, float* dq,
                         hipStream_t s);

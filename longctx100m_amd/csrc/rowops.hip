@@ -18,30 +18,6 @@ __device__ __forceinline__ int64_t stat_index(int64_t row, int N, int H) {
   return (b * H + h) * N + t;
 }
 
-// Weights of the two partials in the merged output.  With m = max(m_a, m_b):
-// l = e^{m_a-m} l_a + e^{m_b-m} l_b and o = (e^{m_a-m} l_a o_a + e^{m_b-m} l_b o_b) / l,
-// which equals carrying the reference's unnormalised (m, l, acc) across the
-// two partials (rs:36-53 applied blockwise).  No key seen on either side:
-// weights 0, l = 0, m = -inf.
-struct MergeW {
-  float wa, wb, m, l;
-};
-__device__ __forceinline__ MergeW merge_weights(float ma, float la, float mb, float lb) {
-  MergeW w;
-  w.m = fmaxf(ma, mb);
-  if (w.m == -INFINITY) {
-    w.wa = w.wb = w.l = 0.f;
-    return w;
-  }
-  const float ea = expf(ma - w.m) * la;
-  const float eb = expf(mb - w.m) * lb;
-  w.l = ea + eb;
-  const float inv = w.l > 0.f ? 1.f / w.l : 0.f;
-  w.wa = ea * inv;
-  w.wb = eb * inv;
-  return w;
-}
-
 // Pass 1 of the merge: output rows.  One thread per 4 consecutive elements
 // when D % 4 == 0 (else per element); statistics are only read here.
 template <int VEC>

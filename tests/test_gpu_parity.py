@@ -82,6 +82,38 @@ def test_fwd_shard_bf16(ra, gpu, case, precise):
     assert np.all(l[~fin] == 0) and np.all(_np(o)[:, ~fin[0].T] == 0)
 
 
+LONG_KEY_CASES = [
+    # b, nq, nk, hq, hkv, q_pos0, causal, valid
+    (2, 64, 66000, 2, 1, 65950, True, None),      # two sub-shards, batch stride, GQA
+    (1, 64, 140000, 1, 1, 139950, True, 70000),   # valid_length in sub-shard 2, sub-shard 3 skipped
+    (1, 64, 70000, 2, 2, 0, False, None),         # non-causal
+    (1, 64, 70000, 1, 1, 30, True, None),         # sub-shard 2 masked for every query
+    (1, 256, 66000, 2, 2, 65800, True, None),     # diagonal inside the second sub-shard
+]
+
+
+@pytest.mark.parametrize("case", LONG_KEY_CASES)
+def test_fwd_shard_long_keys(ra, gpu, case):
+    """A shard of more than 65,536 keys runs as key sub-shards whose results the
+    kernel epilogue LSE-merges into the running state; same bars as above."""
+    b, nq, nk, hq, hkv, qp, causal, valid = case
+    d = 128
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    q = _t(gpu, rng.standard_normal((b, nq, hq, d)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    o, m, l = ra.fwd_shard(q, k, v, q_pos0=qp, k_pos0=0, causal=causal, valid_length=valid)
+    gpu.cuda.synchronize()
+    eo, em, el = dense.attention_fwd(_np(q), _np(k), _np(v), causal=causal, valid_length=valid,
+                                     q_pos0=qp, k_pos0=0)
+    assert norm_rel(_np(o), eo) <= BF16_TOL
+    m, l = _np(m), _np(l)
+    fin = np.isfinite(em)
+    assert np.array_equal(np.isfinite(m), fin)
+    assert np.abs(m[fin] - em[fin]).max() <= 1e-4 * max(1.0, np.abs(em[fin]).max())
+    assert norm_rel(l[fin], el[fin]) <= 1e-4
+
+
 @pytest.mark.parametrize("case", FWD_CASES[:4])
 def test_fwd_shard_fp32(ra, gpu, case):
     nq, nk, hq, hkv, d, qp, kp, causal, valid = case
