@@ -104,27 +104,29 @@ bool pair_active(const lc::Problem& p) {
   return lc::key_end_for(p, p.Nq) > 0;
 }
 
-// Keys per launch of the d=128 forward.  Every workgroup of a head streams
-// the same K/V tiles, and L2 serves them to the workgroups of an XCD only
-// while those stay within a few hundred tiles of each other; over a longer
-// key range they drift apart and the tiles come from HBM again (measured at
-// 1M keys: 16x the memory traffic).  A longer shard therefore runs as
-// sub-shards of this many keys, each LSE-merged into the running (o, m, l) by
-// the kernel's epilogue, as the ring merges its hops.
-constexpr int64_t kFwdKvChunk = 65536;
+// Rows of the streamed operand per launch of the d=128 kernels.  Every
+// workgroup of a head streams the same tiles (K/V in the forward and dQ,
+// Q/dO in dK/dV), and L2 serves them to the workgroups of an XCD only while
+// those stay within a few hundred tiles of each other; over a longer range
+// they drift apart and the tiles come from HBM again (measured on the
+// forward at 1M keys: 16x the memory traffic).  A longer shard therefore runs
+// as sub-shards of this many rows: the forward LSE-merges each into the
+// running (o, m, l) in its epilogue, as the ring merges its hops; dQ, dK and
+// dV accumulate anyway.
+constexpr int64_t kStreamChunk = 65536;
 
 int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v, float* o,
               float* m, float* l, hipStream_t st) {
   hipError_t e = hipSuccess;
   if (use_mfma(p, q, k, v, nullptr) && p.D == 128) {
-    if (p.Nk <= kFwdKvChunk) {
+    if (p.Nk <= kStreamChunk) {
       e = lc::launch_fwd128(p, q, k, v, o, m, l, st);
     } else {
       const size_t row_bytes = (size_t)p.Hkv * p.D * 2;  // bf16 K/V row
       bool first = true;
-      for (int64_t c0 = 0; c0 < p.Nk && e == hipSuccess; c0 += kFwdKvChunk) {
+      for (int64_t c0 = 0; c0 < p.Nk && e == hipSuccess; c0 += kStreamChunk) {
         lc::Problem pc = p;
-        pc.Nk = (int)std::min<int64_t>(kFwdKvChunk, p.Nk - c0);
+        pc.Nk = (int)std::min<int64_t>(kStreamChunk, p.Nk - c0);
         pc.k_pos0 = p.k_pos0 + c0;
         if (!pair_active(pc)) continue;  // the running state is unchanged
         const char* kc = static_cast<const char*>(k) + c0 * row_bytes;
@@ -148,15 +150,47 @@ int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
   const bool mf = use_mfma(p, q, k, v, dout);
   const bool d128 = p.D == 128;
   if (dq != nullptr) {
-    hipError_t e = !mf ? lc::launch_bwd_dq_generic(p, q, k, v, dout, lse2, delta, dq, st)
-                   : d128 ? lc::launch_dq128(p, q, k, v, dout, lse2, delta, dq, st)
-                          : lc::launch_bwd_dq_mfma(p, q, k, v, dout, lse2, delta, dq, st);
+    hipError_t e = hipSuccess;
+    if (!mf) {
+      e = lc::launch_bwd_dq_generic(p, q, k, v, dout, lse2, delta, dq, st);
+    } else if (!d128) {
+      e = lc::launch_bwd_dq_mfma(p, q, k, v, dout, lse2, delta, dq, st);
+    } else if (p.Nk <= kStreamChunk) {
+      e = lc::launch_dq128(p, q, k, v, dout, lse2, delta, dq, st);
+    } else {  // key sub-shards
+      const size_t row_bytes = (size_t)p.Hkv * p.D * 2;
+      for (int64_t c0 = 0; c0 < p.Nk && e == hipSuccess; c0 += kStreamChunk) {
+        lc::Problem pc = p;
+        pc.Nk = (int)std::min<int64_t>(kStreamChunk, p.Nk - c0);
+        pc.k_pos0 = p.k_pos0 + c0;
+        if (!pair_active(pc)) continue;
+        e = lc::launch_dq128(pc, q, static_cast<const char*>(k) + c0 * row_bytes,
+                             static_cast<const char*>(v) + c0 * row_bytes, dout, lse2, delta, dq,
+                             st, p.Nk);
+      }
+    }
     if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dq launch");
   }
   if (dk != nullptr) {
-    hipError_t e = !mf ? lc::launch_bwd_dkdv_generic(p, q, k, v, dout, lse2, delta, dk, dv, st)
-                   : d128 ? lc::launch_dkdv128(p, q, k, v, dout, lse2, delta, dk, dv, st)
-                          : lc::launch_bwd_dkdv_mfma(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    hipError_t e = hipSuccess;
+    if (!mf) {
+      e = lc::launch_bwd_dkdv_generic(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    } else if (!d128) {
+      e = lc::launch_bwd_dkdv_mfma(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    } else if (p.Nq <= kStreamChunk) {
+      e = lc::launch_dkdv128(p, q, k, v, dout, lse2, delta, dk, dv, st);
+    } else {  // query sub-shards
+      const size_t row_bytes = (size_t)p.Hq * p.D * 2;
+      for (int64_t c0 = 0; c0 < p.Nq && e == hipSuccess; c0 += kStreamChunk) {
+        lc::Problem pc = p;
+        pc.Nq = (int)std::min<int64_t>(kStreamChunk, p.Nq - c0);
+        pc.q_pos0 = p.q_pos0 + c0;
+        if (!pair_active(pc)) continue;
+        e = lc::launch_dkdv128(pc, static_cast<const char*>(q) + c0 * row_bytes, k, v,
+                               static_cast<const char*>(dout) + c0 * row_bytes, lse2 + c0,
+                               delta + c0, dk, dv, st, p.Nq);
+      }
+    }
     if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard dk/dv launch");
   }
   return LC_OK;

@@ -45,6 +45,7 @@ struct Bwd128Args {
   float* dk;
   float* dv;
   int Nq, Nk, Hq, Hkv, group, n_tiles;
+  int64_t q_rows, k_rows;  // rows of the whole shards (batch strides; Nq, Nk: this launch's part)
   int64_t q_pos0, k_pos0, valid;
   int causal;
   float sl2;    // scale * log2(e)
@@ -88,10 +89,10 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 
   const int64_t qs = (int64_t)a.Hq * D;
   const int64_t ks = (int64_t)a.Hkv * D;
-  const uint16_t* qbase = a.q + (int64_t)b * a.Nq * qs + (int64_t)h * D;
-  const uint16_t* obase = a.dout + (int64_t)b * a.Nq * qs + (int64_t)h * D;
-  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
-  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* qbase = a.q + (int64_t)b * a.q_rows * qs + (int64_t)h * D;
+  const uint16_t* obase = a.dout + (int64_t)b * a.q_rows * qs + (int64_t)h * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.k_rows * ks + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.k_rows * ks + (int64_t)hk * D;
 
   const int q0 = qt * kDqBM;
   const int qw0 = q0 + wave * kDqQW;
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
       qreg[t] = *reinterpret_cast<const bf16x8*>(qbase + (int64_t)row * qs + 16 * t + 8 * hh);
       doreg[t] = *reinterpret_cast<const bf16x8*>(obase + (int64_t)row * qs + 16 * t + 8 * hh);
     }
-    const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
+    const int64_t si = ((int64_t)b * a.Hq + h) * a.q_rows + row;
     lse = a.lse2[si];
     dl = a.delta[si];
   }
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
   // dQ^T element v of lane l: query qw0 + kc, dim 32*dblk + 8(v/4) + 4hh + v%4.
   const int row = qw0 + kc;
   if (row < a.Nq) {
-    float* dst = a.dq + (((int64_t)b * a.Nq + row) * a.Hq + h) * D;
+    float* dst = a.dq + (((int64_t)b * a.q_rows + row) * a.Hq + h) * D;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
 #pragma unroll
@@ -290,8 +291,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
 
   const int64_t qs = (int64_t)a.Hq * D;
   const int64_t ks = (int64_t)a.Hkv * D;
-  const uint16_t* kbase = a.k + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
-  const uint16_t* vbase = a.v + (int64_t)b * a.Nk * ks + (int64_t)hk * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.k_rows * ks + (int64_t)hk * D;
+  const uint16_t* vbase = a.v + (int64_t)b * a.k_rows * ks + (int64_t)hk * D;
 
   const int k0 = kt * kKvBN;
   const int kw0 = k0 + wave * kKvKW;
@@ -312,11 +313,11 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   t128::RowLoader<kKvBM, 4> ld;
   ld.init(qs, wave, lane);
   auto issue = [&](int hq, int qrow0, int buf) {
-    const uint16_t* qb = a.q + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
-    const uint16_t* ob = a.dout + (int64_t)b * a.Nq * qs + (int64_t)hq * D;
+    const uint16_t* qb = a.q + (int64_t)b * a.q_rows * qs + (int64_t)hq * D;
+    const uint16_t* ob = a.dout + (int64_t)b * a.q_rows * qs + (int64_t)hq * D;
     ld.load(qb, qs, qrow0, a.Nq, t128::lds_addr(smem) + buf * 2 * kKvTile, wave, lane);
     ld.load(ob, qs, qrow0, a.Nq, t128::lds_addr(smem) + (buf * 2 + 1) * kKvTile, wave, lane);
-    const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.Nq;
+    const int64_t sbase = ((int64_t)b * a.Hq + hq) * a.q_rows;
     if (wave == 0) t128::load_f32x64(a.lse2 + sbase, qrow0, a.Nq, t128::lds_addr(stat) + buf * 512, lane);
     if (wave == 1) t128::load_f32x64(a.delta + sbase, qrow0, a.Nq, t128::lds_addr(stat) + buf * 512 + 256, lane);
   };
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   // dK^T / dV^T element v of lane l: key kw0 + l%32, dim 32*dblk + 8(v/4) + 4h + v%4.
   const int row = kw0 + kc;
   if (row < a.Nk) {
-    const int64_t off = (((int64_t)b * a.Nk + row) * a.Hkv + hk) * D;
+    const int64_t off = (((int64_t)b * a.k_rows + row) * a.Hkv + hk) * D;
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
@@ -520,6 +521,8 @@ Bwd128Args make_args(const Problem& p, const void* q, const void* k, const void*
   a.dq = a.dk = a.dv = nullptr;
   a.Nq = p.Nq;
   a.Nk = p.Nk;
+  a.q_rows = p.Nq;
+  a.k_rows = p.Nk;
   a.Hq = p.Hq;
   a.Hkv = p.Hkv;
   a.group = p.Hq / p.Hkv;
@@ -537,9 +540,10 @@ Bwd128Args make_args(const Problem& p, const void* q, const void* k, const void*
 
 hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const void* v,
                         const void* dout, const float* lse2, const float* delta, float* dq,
-                        hipStream_t s) {
+                        hipStream_t s, int64_t k_rows) {
   if (p.D != D) return hipErrorInvalidValue;
   Bwd128Args a = make_args(p, q, k, v, dout, lse2, delta);
+  if (k_rows >= 0) a.k_rows = k_rows;
   a.dq = dq;
   a.n_tiles = (p.Nq + kDqBM - 1) / kDqBM;
   hipLaunchKernelGGL(dq128_kernel, dim3(a.n_tiles * p.Hq * p.B), dim3(256), 0, s, a);
@@ -548,9 +552,10 @@ hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const vo
 
 hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
                           const void* dout, const float* lse2, const float* delta, float* dk,
-                          float* dv, hipStream_t s) {
+                          float* dv, hipStream_t s, int64_t q_rows) {
   if (p.D != D) return hipErrorInvalidValue;
   Bwd128Args a = make_args(p, q, k, v, dout, lse2, delta);
+  if (q_rows >= 0) a.q_rows = q_rows;
   a.dk = dk;
   a.dv = dv;
   a.n_tiles = (p.Nk + kKvBN - 1) / kKvBN;

@@ -42,12 +42,16 @@ bool mfma_supported(const Problem& p);
 hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const void* v, float* o,
                          float* m, float* l, hipStream_t s, int64_t kv_rows = -1,
                          bool accumulate = false);
+// The backward can run on a sub-shard too (results accumulate into dq, dk,
+// dv anyway): dQ on a key sub-shard (k, v at its first key, k_rows = keys of
+// the whole shard), dK/dV on a query sub-shard (q, dout, lse2, delta at its
+// first query, q_rows = queries of the whole shard).  -1: p's own count.
 hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const void* v,
                         const void* dout, const float* lse2, const float* delta, float* dq,
-                        hipStream_t s);
+                        hipStream_t s, int64_t k_rows = -1);
 hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
                           const void* dout, const float* lse2, const float* delta, float* dk,
-                          float* dv, hipStream_t s);
+                          float* dv, hipStream_t s, int64_t q_rows = -1);
 
 // head_dim 64 (and 128 on request): register-staged tiles (fwd_mfma.hip, bwd_mfma.hip).
 hipError_t launch_fwd_mfma(const Problem& p, const void* q, const void* k, const void* v, float* o,

@@ -167,6 +167,41 @@ def test_bwd_shard(ra, gpu, case, dtype_name, precise):
     assert norm_rel(_np(dv), edv) <= tol
 
 
+LONG_BWD_CASES = [
+    # b, nq, nk, hq, hkv, q_pos0, k_pos0, causal
+    (2, 32, 70000, 1, 1, 69980, 0, True),       # dQ over key sub-shards, batch stride
+    (1, 70000, 64, 2, 2, 0, 0, True),           # dK/dV over query sub-shards
+    (1, 70000, 64, 1, 1, 0, 65600, True),       # first query sub-shard sees no key (skipped)
+    (2, 66000, 32, 2, 1, 0, 0, False),          # dK/dV sub-shards, GQA group walk, batch stride
+]
+
+
+@pytest.mark.parametrize("case", LONG_BWD_CASES)
+def test_bwd_shard_long_stream(ra, gpu, case):
+    """More than 65,536 streamed rows (keys for dQ, queries for dK/dV) run as
+    sub-shards accumulating into the same gradients; bf16 bar as above."""
+    b, nq, nk, hq, hkv, qp, kp, causal = case
+    d = 128
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    q = _t(gpu, rng.standard_normal((b, nq, hq, d)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    do = _t(gpu, rng.standard_normal((b, nq, hq, d)), gpu.bfloat16)
+    kw = dict(q_pos0=qp, k_pos0=kp, causal=causal)
+    o32, m, l = ra.fwd_shard(q, k, v, **kw)
+    out = o32.to(gpu.bfloat16)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    dq = gpu.zeros((b, nq, hq, d), dtype=gpu.float32, device="cuda")
+    dk = gpu.zeros((b, nk, hkv, d), dtype=gpu.float32, device="cuda")
+    dv = gpu.zeros_like(dk)
+    ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, **kw)
+    gpu.cuda.synchronize()
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **kw)
+    assert norm_rel(_np(dq), edq) <= BF16_TOL
+    assert norm_rel(_np(dk), edk) <= BF16_TOL
+    assert norm_rel(_np(dv), edv) <= BF16_TOL
+
+
 def test_merge_is_order_invariant(ra, gpu):
     rng = np.random.default_rng(5)
     nq, hq, d = 192, 2, 128
