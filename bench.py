@@ -61,6 +61,9 @@ def parse():
                     help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
                          "against its diagonal block plus one full incoming 1M-token KV shard; "
                          "prints its own JSON line with TFLOP/s and the HBM footprint")
+    ap.add_argument("--bwd-recompute", action="store_true",
+                    help="backward without dS sharing: the dQ kernel recomputes S and dP "
+                         "instead of reading the dS the dK/dV kernel stored")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -133,8 +136,10 @@ def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
         per = json.loads(block)["traffic_bytes_per_full_hop"]
     except (OSError, IndexError, KeyError, ValueError):
         return None
-    names = [k for k in per if k in rl_kernel]
-    return sum(per[k] for k in names) if names else None
+    names = [part.split()[0] for part in rl_kernel.split(" + ")]
+    if not all(k in per for k in names):
+        return None  # a kernel of this roofline has no committed traffic measurement
+    return sum(per[k] for k in names)
 
 
 def long_shard(args, torch, ra) -> int:
@@ -474,6 +479,12 @@ def main() -> int:
     dq_acc = torch.empty(1, n, h, d, **f32)
     dk_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
     dv_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
+    ws = None
+    if not args.bwd_recompute:
+        ws_bytes = ra.bwd_shard_workspace_bytes(q, ks[0])
+        if ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            log(f"dS exchange workspace: {ws_bytes / 2**30:.1f} GiB")
 
     timers = {}
 
@@ -513,6 +524,11 @@ def main() -> int:
             dv_acc[b].zero_()
         for b in owners:
             tag = "diag" if b == rank else "full"
+            if ws is not None:  # dK/dV stores dS, dQ reads it back
+                timed(f"bwd_{tag}", lambda b=b: ra.bwd_shard(
+                    q, ks[b], vs[b], dout, lse2, delta, q_pos0=q_pos0, k_pos0=b * n,
+                    dq_acc=dq_acc, dk_acc=dk_acc[b], dv_acc=dv_acc[b], workspace=ws))
+                continue
             timed(f"dq_{tag}", lambda b=b: ra.bwd_shard(q, ks[b], vs[b], dout, lse2, delta,
                                                         q_pos0=q_pos0, k_pos0=b * n,
                                                         dq_acc=dq_acc))
@@ -556,11 +572,16 @@ def main() -> int:
     # Dominant kernel class by time per step; roofline against the bf16 MFMA peak.
     tot = {k: v["avg_ms"] * v["launches_per_step"] for k, v in kern.items()}
     fwd_t = tot.get("fwd_full", 0.0) + tot.get("fwd_diag", 0.0)
-    bwd_t = sum(tot.get(k, 0.0) for k in ("dq_full", "dq_diag", "dkdv_full", "dkdv_diag"))
+    bwd_t = sum(tot.get(k, 0.0) for k in ("dq_full", "dq_diag", "dkdv_full", "dkdv_diag",
+                                          "bwd_full", "bwd_diag"))
     if n_full > 0 and bwd_t >= fwd_t:
-        pair_ms = kern["dq_full"]["avg_ms"] + kern["dkdv_full"]["avg_ms"]
+        if "bwd_full" in kern:
+            pair_ms = kern["bwd_full"]["avg_ms"]
+            rl_kernel = "dkdv128_kernel + dqds128_kernel (one full hop)"
+        else:
+            pair_ms = kern["dq_full"]["avg_ms"] + kern["dkdv_full"]["avg_ms"]
+            rl_kernel = "dq128_kernel + dkdv128_kernel (one full hop)"
         achieved = 2.5 * unit / (pair_ms * 1e-3) / 1e12
-        rl_kernel = "dq128_kernel + dkdv128_kernel (one full hop)"
         rl_units = f"2.5 x 4*N*N*H*d = {2.5 * unit / 1e12:.3f} TFLOP per full hop"
     elif n_full > 0:
         achieved = unit / (kern["fwd_full"]["avg_ms"] * 1e-3) / 1e12

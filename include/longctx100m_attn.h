@@ -134,6 +134,23 @@ int lc_attn_bwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
                       const float* delta, float* dq_acc, float* dk_acc, float* dv_acc,
                       void* stream);
 
+/* The same hop backward with a caller-owned workspace, replacing the same
+ * reference lines (rs:383-409 and rs:433-454) when one rank computes both
+ * dQ and dK/dV of a shard pair, as a ring that sends dK/dV back does.  With
+ * dq_acc, dk_acc and dv_acc all set, d = 128 on the bf16 MFMA path and a
+ * 256-byte-aligned workspace, the dK/dV kernel stores dS (bf16) in the
+ * workspace and dQ is computed from it, without recomputing the scores.  The
+ * workspace holds the dS of a chunk of query rows at a time: the full size
+ * from lc_attn_bwd_shard_workspace_bytes runs the pair in chunks of up to
+ * 65,536 rows; a smaller one runs smaller chunks (multiples of 128 rows).
+ * With no usable workspace, or other shapes, this is lc_attn_bwd_shard.
+ * Results agree with lc_attn_bwd_shard up to fp32 summation order. */
+size_t lc_attn_bwd_shard_workspace_bytes(const lc_attn_shape_t* shape);
+int lc_attn_bwd_shard_ws(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                         const void* k, const void* v, const void* dout, const float* lse2,
+                         const float* delta, float* dq_acc, float* dk_acc, float* dv_acc,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- emulated ring (one GPU, ordered loop over KV shards in HBM) ------------ */
 
 /* Ring geometry: world equal shards of local_tokens tokens. */

@@ -97,6 +97,10 @@ SIGNATURES = {
                                        c_void_p, c_void_p]),
     "lc_attn_bwd_shard": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "lc_attn_bwd_shard_workspace_bytes": (c_size_t, [_S]),
+    "lc_attn_bwd_shard_ws": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                     c_void_p]),
     "lc_ring_fwd_workspace_bytes": (c_size_t, [_R]),
     "lc_ring_bwd_workspace_bytes": (c_size_t, [_R]),
     "lc_ring_fwd_with_stats": (c_int, [_R, _vpp, _vpp, _vpp, c_void_p, c_void_p, c_void_p,

@@ -56,6 +56,7 @@ SCRATCH_LIMITS = {
     "fwd128_kernel": 0,
     "dq128_kernel": 0,
     "dkdv128_kernel": 64,
+    "dqds128_kernel": 0,
     "decode128_kernel": 0,
 }
 

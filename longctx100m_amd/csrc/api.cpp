@@ -196,6 +196,64 @@ int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
   return LC_OK;
 }
 
+// dS sharing (d = 128 on the bf16 MFMA path, dQ and dK/dV both requested, a
+// workspace given): the dK/dV kernel stores the dS it forms and the dQ
+// kernel reads it back, so dQ costs one GEMM instead of three (S, dP and dQ).
+// The workspace holds the dS of one chunk of query rows at a time; chunks are
+// multiples of 128 rows (one dQ workgroup) of at most kStreamChunk rows.
+// Returns the chunk's row count, 0 when the shape or workspace does not allow
+// it.
+int64_t ds_chunk_rows(const lc::Problem& p, size_t ws_bytes) {
+  const int64_t nkb = (p.Nk + 31) / 32;
+  const size_t per_tile = (size_t)p.B * p.Hq * nkb * lc::kDsBlockBytes;  // 32 query rows
+  if (per_tile == 0) return 0;
+  int64_t rows = (int64_t)(ws_bytes / per_tile) * 32;
+  rows = std::min<int64_t>(rows, kStreamChunk);
+  rows = rows >= p.Nq ? p.Nq : rows / 128 * 128;
+  // block indices of one chunk are 32-bit in the kernels
+  if ((int64_t)p.B * p.Hq * ((rows + 31) / 32) * nkb >= (int64_t)1 << 31) return 0;
+  return rows;
+}
+
+size_t ds_workspace_bytes(const lc::Problem& p) {
+  const int64_t rows = std::min<int64_t>(p.Nq, kStreamChunk);
+  return (size_t)p.B * p.Hq * ((rows + 31) / 32) * ((p.Nk + 31) / 32) * lc::kDsBlockBytes;
+}
+
+bool ds_path(const lc::Problem& p, const void* q, const void* k, const void* v, const void* dout) {
+  return p.D == 128 && use_mfma(p, q, k, v, dout);
+}
+
+int bwd_shard_ds(const lc::Problem& p, int64_t chunk, const void* q, const void* k, const void* v,
+                 const void* dout, const float* lse2, const float* delta, float* dq, float* dk,
+                 float* dv, uint16_t* ds, hipStream_t st) {
+  const size_t qrow_bytes = (size_t)p.Hq * p.D * 2;  // bf16 Q / dO row
+  const size_t krow_bytes = (size_t)p.Hkv * p.D * 2;
+  const int nkb = (p.Nk + 31) / 32;
+  for (int64_t c0 = 0; c0 < p.Nq; c0 += chunk) {
+    lc::Problem pc = p;
+    pc.Nq = (int)std::min<int64_t>(chunk, p.Nq - c0);
+    pc.q_pos0 = p.q_pos0 + c0;
+    if (!pair_active(pc)) continue;
+    hipError_t e = lc::launch_dkdv128(pc, static_cast<const char*>(q) + c0 * qrow_bytes, k, v,
+                                      static_cast<const char*>(dout) + c0 * qrow_bytes, lse2 + c0,
+                                      delta + c0, dk, dv, st, p.Nq, ds);
+    if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard_ws dk/dv launch");
+    const int nqt = (pc.Nq + 31) / 32;
+    float* dqc = dq + c0 * p.Hq * p.D;
+    for (int64_t k0 = 0; k0 < p.Nk && e == hipSuccess; k0 += kStreamChunk) {  // key sub-shards
+      lc::Problem pk = pc;
+      pk.Nk = (int)std::min<int64_t>(kStreamChunk, p.Nk - k0);
+      pk.k_pos0 = p.k_pos0 + k0;
+      if (!pair_active(pk)) continue;
+      e = lc::launch_dqds128(pk, static_cast<const char*>(k) + k0 * krow_bytes,
+                             ds + (k0 / 32) * 1024, nqt, nkb, dqc, st, p.Nk, p.Nq);
+    }
+    if (e != hipSuccess) return hip_error(e, "lc_attn_bwd_shard_ws dq launch");
+  }
+  return LC_OK;
+}
+
 // ---- ring descriptors ---------------------------------------------------------
 
 int check_ring(const lc_ring_desc_t* d) {
@@ -389,6 +447,39 @@ int lc_attn_bwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
   if (!pair_active(p)) return LC_OK;
   return bwd_shard(p, q, k, v, dout, lse2, delta, dq_acc, dk_acc, dv_acc,
                    static_cast<hipStream_t>(stream));
+}
+
+size_t lc_attn_bwd_shard_workspace_bytes(const lc_attn_shape_t* shape) {
+  if (check_shape(shape) != LC_OK) return 0;
+  const lc::Problem p = make_problem(shape, nullptr);
+  if (p.D != 128 || !lc::mfma_supported(p)) return 0;
+  return ds_workspace_bytes(p);
+}
+
+int lc_attn_bwd_shard_ws(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                         const void* k, const void* v, const void* dout, const float* lse2,
+                         const float* delta, float* dq_acc, float* dk_acc, float* dv_acc,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!q || !k || !v || !dout || !lse2 || !delta)
+    return set_error(LC_ERR_INVALID, "null pointer argument");
+  if ((dk_acc == nullptr) != (dv_acc == nullptr))
+    return set_error(LC_ERR_INVALID, "dk_acc and dv_acc must both be set or both be NULL");
+  if (mask && mask->valid_length < -1)
+    return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
+  if (workspace == nullptr && workspace_bytes != 0)
+    return set_error(LC_ERR_INVALID, "workspace is NULL but workspace_bytes is not 0");
+  const lc::Problem p = make_problem(shape, mask);
+  if (!pair_active(p)) return LC_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dq_acc && dk_acc && workspace && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0 &&
+      ds_path(p, q, k, v, dout)) {
+    const int64_t chunk = ds_chunk_rows(p, workspace_bytes);
+    if (chunk > 0)
+      return bwd_shard_ds(p, chunk, q, k, v, dout, lse2, delta, dq_acc, dk_acc, dv_acc,
+                          static_cast<uint16_t*>(workspace), st);
+  }
+  return bwd_shard(p, q, k, v, dout, lse2, delta, dq_acc, dk_acc, dv_acc, st);
 }
 
 size_t lc_ring_fwd_workspace_bytes(const lc_ring_desc_t* desc) {

@@ -20,6 +20,10 @@
 //           LSE and delta double-buffered in LDS.
 //             S = Q K^T, dP = dO V^T       (A = Q, dO rows)
 //             dV^T += dO^T P, dK^T += Q^T dS  (A = dO^T, Q^T: transposed reads)
+// and, when one caller wants dQ and dK/dV of the same shard pair and gives a
+// workspace, a dS-sharing pair: dkdv128 also stores its dS (bf16), and
+//   dqds128 Q-stationary like dq128, but dQ^T += K^T dS^T with dS read back
+//           (one GEMM instead of three; HBM-bound on the dS read).
 // Tiles are swizzled row-major and filled by direct global->LDS loads
 // (tile128.h); each score accumulator's C layout is reused as the B operand
 // of the following product.
@@ -50,7 +54,29 @@ struct Bwd128Args {
   int causal;
   float sl2;    // scale * log2(e)
   float scale;  // D^-1/2
+  // dS exchange blocks (dkdv128 writes them when ds is set, dqds128 reads
+  // them): ds_nqt query tiles x ds_nkb key blocks per (batch, query head).
+  uint16_t* ds;
+  int ds_nqt, ds_nkb;
 };
+
+// dS exchange layout.  dS (bf16, unscaled) of query tile qt (32 queries) and
+// key block kb (32 keys) of head (b, hq) is a 2 KB block at element
+// ((((b * Hq + hq) * nqt + qt) * nkb + kb) * 1024.  The dK/dV lane (key c,
+// half h = lane / 32) holds k-step u of its dS B operand as 8 bf16: queries
+// 16u + row(h, p, t) of tr32_off in slot 4p + t.  It stores them at byte
+//   1024 u + 16 (ds_slot(c, h) ^ 8u)
+// of the block, so one wave instruction writes 1 KB contiguously.  The dQ
+// kernel reads the blocks back with transposed LDS reads (the key becomes the
+// k index): the 16-byte slots of one transposed read (fixed key bits 0, 2, 4,
+// varying bits 1, 3, the half and u) fall on 16 distinct slots modulo 256
+// bytes, so the reads are free of bank conflicts.
+__device__ __forceinline__ int ds_slot(int key, int half) {
+  return ((key >> 1) & 1) | (((key >> 3) & 1) << 1) | (half << 2) | ((key & 1) << 3) |
+         (((key >> 2) & 1) << 4) | (((key >> 4) & 1) << 5);
+}
+constexpr int kDsBlockElems = 1024;
+constexpr int kDsBlockKeys = 32;  // keys per exchange block (= dK/dV keys per wave)
 
 // ------------------------------------------------------------------- dQ --
 
@@ -256,6 +282,163 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
   }
 }
 
+// ------------------------------------------------- dQ from stored dS --
+
+// dQ^T += K^T dS^T with dS read back from the exchange blocks dkdv128 wrote
+// for the same (query shard, KV shard) pair: no score recomputation, one
+// GEMM.  Workgroup = 4 waves x 32 queries of one (batch, query head); 64-key
+// tiles of K (shared, LDS DMA) and each wave's two dS blocks of the tile
+// (its own, LDS DMA), one barrier per tile.
+//   A = K^T (transposed reads of the K tile, tr32_off), B = dS^T (transposed
+//   reads of the dS blocks, same key order)
+// Column j of the accumulator is query qw0 + ds_query(j): the transposed read
+// hands lane c of a 16-lane group element c % 4 of the 8-byte chunk c / 4 of
+// a stored row, and a stored row of half h holds queries 16u + row(h, p, t).
+// A tile block that dkdv128 skipped (keys past the shard or, causal, after
+// every query of the wave) is replaced by zeros; inside a written block every
+// masked score already has dS = 0.
+constexpr int kDsWaveBytes = 2 * 2 * kDsBlockElems;  // a wave's two blocks of one tile
+constexpr int kDsStages = 3;  // dS tiles in LDS: the one in use and two in flight
+
+__device__ __forceinline__ int ds_query(int j) {
+  const int c = j & 15, cb = j >> 4;
+  return 16 * (c >> 3) + 4 * cb + ((c >> 2) & 1) + 2 * (c & 1) + 8 * ((c >> 1) & 1);
+}
+
+// LDS: K double-buffered (one tile ahead), dS in kDsStages buffers (two tiles
+// ahead, the kernel streams them from HBM): 80 KB, two workgroups per CU.
+__global__ __launch_bounds__(256, 2) void dqds128_kernel(Bwd128Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kDqTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t dsbuf[kDsStages][4][kDsWaveBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int kc = lane & 31;
+  const int hh = lane >> 5;
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = a.n_tiles - 1 - (L % a.n_tiles);
+  const int bh = L / a.n_tiles;
+  const int h = bh % a.Hq;
+  const int b = bh / a.Hq;
+  const int hk = h / a.group;
+
+  const int64_t ks = (int64_t)a.Hkv * D;
+  const uint16_t* kbase = a.k + (int64_t)b * a.k_rows * ks + (int64_t)hk * D;
+
+  const int q0 = qt * kDqBM;
+  const int qw0 = q0 + wave * kDqQW;
+
+  const int q_end = min(q0 + kDqBM, a.Nq);
+  int64_t kend = a.Nk;
+  if (a.causal) kend = min(kend, a.q_pos0 + q_end - a.k_pos0);
+  kend = min(kend, a.valid - a.k_pos0);
+  const int ntiles = kend > 0 ? (int)((kend + kDqBN - 1) / kDqBN) : 0;
+  if (ntiles == 0) return;
+  int nt_w = 0;
+  if (qw0 < a.Nq) {
+    int64_t kw = kend;
+    if (a.causal) kw = min(kw, a.q_pos0 + min(qw0 + kDqQW, a.Nq) - a.k_pos0);
+    nt_w = kw > 0 ? (int)((kw + kDqBN - 1) / kDqBN) : 0;
+  }
+  const int nkb = (a.Nk + kDsBlockKeys - 1) / kDsBlockKeys;  // this launch's key blocks
+  // The wave's row of exchange blocks (only formed when the wave has tiles).
+  const uint16_t* dsrow = nt_w > 0
+      ? a.ds + (((int64_t)b * a.Hq + h) * a.ds_nqt + qw0 / kDqQW) * a.ds_nkb * kDsBlockElems
+      : a.ds;
+
+  const uint32_t kbuf_lds = t128::lds_addr(kbuf);
+  const uint32_t ds_lds = t128::lds_addr(dsbuf) + wave * kDsWaveBytes;
+  t128::RowLoader<kDqBN, 4> ld;
+  ld.init(ks, wave, lane);
+  // dS of tile j (blocks 2j, 2j+1) as exactly four DMA instructions, so the
+  // wait for the older loads is a fixed vmcnt(4); a missing block 2j+1 (past
+  // the keys) re-reads block 2j, and its operand is zeroed below.
+  auto load_ds = [&](int j) {
+    if (j >= nt_w) return false;
+    const int nb = min(2, nkb - 2 * j);
+    const uint16_t* src = dsrow + (int64_t)(2 * j) * kDsBlockElems;
+    const uint32_t dst = ds_lds + (j % kDsStages) * 4 * kDsWaveBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int si = i < 2 * nb ? i : i - 2;
+      t128::dma_b128_nt(src + si * (kDsBlockElems / 2), 16u * lane, dst + i * 1024);
+    }
+    return true;
+  };
+  ld.load(kbase, ks, 0, a.Nk, kbuf_lds, wave, lane);
+  load_ds(0);
+  bool ahead = load_ds(1);  // the last loads issued are a dS tile not needed yet
+
+  // B operand read of k-step 0, k-half 0: lane (group G, index i) addresses
+  // row key(hh, 0, t) of half G % 2, chunk g = i % 4 (u = g / 2, byte 8 (g % 2)).
+  int dsoff0;
+  {
+    const int i = lane & 15, t = i >> 2, g = i & 3, u = g >> 1, cb = (lane >> 4) & 1;
+    dsoff0 = u * 1024 + 16 * ((t | (cb << 2) | (hh << 4)) | (u << 3)) + 8 * (g & 1);
+  }
+  const int toff0 = t128::tr32_off(0, lane), toff1 = t128::tr32_off(1, lane);
+  const int64_t wq_last = a.q_pos0 + qw0 + kDqQW - 1;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+
+  for (int j = 0; j < ntiles; ++j) {
+    if (ahead)
+      t128::wait_vmem_but<4>();  // K_j and dS_j, not dS_{j+1}
+    else
+      t128::wait_vmem();
+    __syncthreads();
+    if (j + 1 < ntiles)
+      ld.load(kbase, ks, (j + 1) * kDqBN, a.Nk, kbuf_lds + ((j + 1) & 1) * kDqTile, wave, lane);
+    ahead = load_ds(j + 2);
+    if (j >= nt_w) continue;
+    const uint8_t* kt = kbuf[j & 1];
+    const uint8_t* dt = dsbuf[j % kDsStages][wave];
+    // block 2j + 1 was not written by dkdv128: past the keys, or after every query
+    const int64_t k1 = (int64_t)j * kDqBN + kDsBlockKeys;
+    const bool skip1 = k1 >= a.Nk || (a.causal && a.k_pos0 + k1 > wq_last);
+    const int so0 = opaque(dsoff0), so1 = so0 ^ 128;
+    const int to0 = opaque(toff0), to1 = opaque(toff1);
+    bf16x8 B[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ko = (u >> 1) * 2 * kDsBlockElems + (u & 1) * 512;
+      B[u] = concat_bf16x4(t128::ds_read_tr(dt + so0 + ko), t128::ds_read_tr(dt + so1 + ko));
+    }
+    if (skip1) B[2] = B[3] = bf16x8{};
+    auto fetch = [&](int i) {  // K^T of keys 16(i/4) .., dims 32 (i%4) ..
+      const int o0 = (to0 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+      const int o1 = (to1 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+      return concat_bf16x4(t128::ds_read_tr(kt + o0), t128::ds_read_tr(kt + o1));
+    };
+    bf16x8 A[2] = {fetch(0), fetch(1)};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i & 3] = mfma32x32x16(A[i & 1], B[i >> 2], acc[i & 3]);
+      if (i + 2 < 16) A[i & 1] = fetch(i + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // dQ^T element v of lane l: query qw0 + ds_query(l % 32), dim 32 dblk + 8(v/4) + 4hh + v%4.
+  const int row = qw0 + ds_query(kc);
+  if (nt_w > 0 && row < a.Nq) {
+    float* dst = a.dq + (((int64_t)b * a.q_rows + row) * a.Hq + h) * D;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        f32x4* p = reinterpret_cast<f32x4*>(dst + 32 * d + 8 * w + 4 * hh);
+        const f32x4 v4 = {acc[d][4 * w], acc[d][4 * w + 1], acc[d][4 * w + 2], acc[d][4 * w + 3]};
+        *p = *p + v4 * a.scale;
+      }
+  }
+}
+
 // ---------------------------------------------------------------- dK/dV --
 
 constexpr int kKvKW = 32;
@@ -337,6 +520,11 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     vld.init(ks, wave, lane);
     vld.load(vbase, ks, k0, a.Nk, t128::lds_addr(v_lds), wave, lane);
   }
+  // K^T is in VGPRs from here on.  Without this wait the compiler (which
+  // cannot tell how many vector memory operations the loop's waits leave
+  // pending) would wait for the K loads before each S step, i.e. for every
+  // load and store issued before that point.
+  t128::wait_vmem();
 
   // Row l%32 of a Q/dO tile, dims 16t + 8h .. +7, is roff0 ^ (32 t); the
   // wave's V rows are the same offsets in the wave's part of the V tile.
@@ -358,6 +546,7 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   //   j 24-31  dK^T += Q^T dS       (u, dblk) = ((j-24)/4, (j-24)%4)
   // P = exp2(S sl2 - lse2) is formed on the VALU during the dP steps, and
   // dS = P (dP - delta) during the dV steps, beside the running MFMAs.
+  bf16x8 ds_keep[2];  // the last tile's packed dS (both k-steps), stored at the next step's top
   auto tile = [&](auto masked_tag, int buf, int cthr, int kmax, int qmax) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     const uint8_t* qt_ = smem[buf][0];
@@ -454,29 +643,63 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
         db[u] = pack_bf16x8(f32x4{dpv[8 * u], dpv[8 * u + 2], dpv[8 * u + 4], dpv[8 * u + 6]},
                             f32x4{dpv[8 * u + 1], dpv[8 * u + 3], dpv[8 * u + 5], dpv[8 * u + 7]});
       }
+      // k-step u of dS to the exchange block right after its pack, so that the
+      // store has read its data long before the registers are reused
+      if (j == 31) {  // stored at the next step's top
+        ds_keep[0] = db[0];
+        ds_keep[1] = db[1];
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  int cur_q = qstart;                  // step being computed
+  int cur_q = qstart, cur_hq = hq0;    // step being computed
   int nxt_hq = hq0, nxt_q = qstart;    // step being prefetched
+  // dS stores: a tile's dS is stored at the top of the next step, after that
+  // step's tile loads, so the wait for those loads at the following top does
+  // not include the stores (vector memory operations complete in issue order,
+  // and the stores take longer): they have two steps to complete.
+  bool stored = false;  // this step's top issued the two dS stores (after its loads)
+  int pend = -1;        // exchange block of ds_keep, not yet stored
+  auto store_ds = [&](int blkid) {
+    const int dsl = ds_slot(opaque(kc), opaque(h));
+    typedef __attribute__((address_space(1))) bf16x8 gbl_bf16x8;  // global, not flat
+    uint8_t* blk = reinterpret_cast<uint8_t*>(a.ds + (int64_t)blkid * kDsBlockElems);
+    __builtin_nontemporal_store(ds_keep[0], (gbl_bf16x8*)(blk + 16 * dsl));
+    __builtin_nontemporal_store(ds_keep[1], (gbl_bf16x8*)(blk + 1024 + 16 * (dsl ^ 8)));
+  };
   for (int step = 0; step < nsteps; ++step) {
-    t128::wait_vmem();
+    if (stored)
+      t128::wait_vmem_but<2>();  // the tile loads, not the stores issued after them
+    else
+      t128::wait_vmem();
     __syncthreads();
+    stored = false;
     nxt_q += kKvBM;
     if (nxt_q >= a.Nq) {
       nxt_q = qstart;
       ++nxt_hq;
     }
     if (step + 1 < nsteps) issue(nxt_hq, nxt_q, (step + 1) & 1);
-    const int qrow0 = cur_q;
+    if (pend >= 0) {  // the previous tile's dS, after the loads
+      store_ds(pend);
+      stored = true;
+      pend = -1;
+    }
+    const int qrow0 = cur_q, hq_c = cur_hq;
     cur_q += kKvBM;
-    if (cur_q >= a.Nq) cur_q = qstart;
+    if (cur_q >= a.Nq) {
+      cur_q = qstart;
+      ++cur_hq;
+    }
     const int64_t qp_first = a.q_pos0 + qrow0;
     const int64_t qp_last = qp_first + kKvBM - 1;
     if (kw0 >= a.Nk) continue;
     if (a.causal && wk_first > qp_last) continue;
     const int buf = step & 1;
+    const int dsblk = a.ds == nullptr ? -1
+        : ((b * a.Hq + hq_c) * a.ds_nqt + qrow0 / kKvBM) * a.ds_nkb + kw0 / kKvKW;
+    pend = dsblk;
     if ((a.causal && wk_last > qp_first) || wk_last >= a.valid || kw0 + kKvKW > a.Nk ||
         qrow0 + kKvBM > a.Nq) {
       const int64_t ct = qp_first - wk_first;
@@ -489,6 +712,7 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
       tile(std::false_type{}, buf, 0, kKvKW, kKvBM);
     }
   }
+  if (pend >= 0) store_ds(pend);
 
   // dK^T / dV^T element v of lane l: key kw0 + l%32, dim 32*dblk + 8(v/4) + 4h + v%4.
   const int row = kw0 + kc;
@@ -533,6 +757,8 @@ Bwd128Args make_args(const Problem& p, const void* q, const void* k, const void*
   a.causal = p.causal ? 1 : 0;
   a.sl2 = p.scale * kLog2e;
   a.scale = p.scale;
+  a.ds = nullptr;
+  a.ds_nqt = a.ds_nkb = 0;
   return a;
 }
 
@@ -552,14 +778,34 @@ hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const vo
 
 hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
                           const void* dout, const float* lse2, const float* delta, float* dk,
-                          float* dv, hipStream_t s, int64_t q_rows) {
+                          float* dv, hipStream_t s, int64_t q_rows, uint16_t* ds) {
   if (p.D != D) return hipErrorInvalidValue;
   Bwd128Args a = make_args(p, q, k, v, dout, lse2, delta);
   if (q_rows >= 0) a.q_rows = q_rows;
   a.dk = dk;
   a.dv = dv;
+  if (ds != nullptr) {
+    a.ds = ds;
+    a.ds_nqt = (p.Nq + kKvBM - 1) / kKvBM;
+    a.ds_nkb = (p.Nk + kDsBlockKeys - 1) / kDsBlockKeys;
+  }
   a.n_tiles = (p.Nk + kKvBN - 1) / kKvBN;
   hipLaunchKernelGGL(dkdv128_kernel, dim3(a.n_tiles * p.Hkv * p.B), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dqds128(const Problem& p, const void* k, const uint16_t* ds, int ds_nqt,
+                          int ds_nkb, float* dq, hipStream_t s, int64_t k_rows, int64_t q_rows) {
+  if (p.D != D) return hipErrorInvalidValue;
+  Bwd128Args a = make_args(p, nullptr, k, nullptr, nullptr, nullptr, nullptr);
+  if (k_rows >= 0) a.k_rows = k_rows;
+  if (q_rows >= 0) a.q_rows = q_rows;
+  a.dq = dq;
+  a.ds = const_cast<uint16_t*>(ds);
+  a.ds_nqt = ds_nqt;
+  a.ds_nkb = ds_nkb;
+  a.n_tiles = (p.Nq + kDqBM - 1) / kDqBM;
+  hipLaunchKernelGGL(dqds128_kernel, dim3(a.n_tiles * p.Hq * p.B), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -51,7 +51,17 @@ hipError_t launch_dq128(const Problem& p, const void* q, const void* k, const vo
                         hipStream_t s, int64_t k_rows = -1);
 hipError_t launch_dkdv128(const Problem& p, const void* q, const void* k, const void* v,
                           const void* dout, const float* lse2, const float* delta, float* dk,
-                          float* dv, hipStream_t s, int64_t q_rows = -1);
+                          float* dv, hipStream_t s, int64_t q_rows = -1, uint16_t* ds = nullptr);
+// dS sharing: launch_dkdv128 with ds set also writes every dS block it forms
+// (ceil(Nq/32) x ceil(Nk/32) blocks of 2 KB per (batch, query head), layout
+// in bwd128.hip); launch_dqds128 then adds dQ = scale dS K from those blocks
+// for the same problem, or for a key sub-shard of it: k and ds at the
+// sub-shard's first key (ds + (c0 / 32) * 1024), ds_nkb the row length of the
+// whole shard, k_rows / q_rows the batch strides.
+constexpr size_t kDsBlockBytes = 2048;
+hipError_t launch_dqds128(const Problem& p, const void* k, const uint16_t* ds, int ds_nqt,
+                          int ds_nkb, float* dq, hipStream_t s, int64_t k_rows = -1,
+                          int64_t q_rows = -1);
 
 // head_dim 64 (and 128 on request): register-staged tiles (fwd_mfma.hip, bwd_mfma.hip).
 hipError_t launch_fwd_mfma(const Problem& p, const void* q, const void* k, const void* v, float* o,

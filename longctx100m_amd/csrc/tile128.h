@@ -87,6 +87,14 @@ __device__ __forceinline__ void dma_b128(const void* base, uint32_t off, uint32_
                : "memory");
 }
 
+// Same, non-temporal (streaming data read once: L2 does not keep it).
+__device__ __forceinline__ void dma_b128_nt(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+               :
+               : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
 __device__ __forceinline__ void dma_b32(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
                :
@@ -164,6 +172,14 @@ __device__ __forceinline__ void load_f32x64(const float* base, int i0, int n, ui
 // insertion knows every earlier vector memory load has completed here (it does
 // not parse inline asm).  Immediate: vmcnt 0, expcnt 7, lgkmcnt 15.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// s_waitcnt vmcnt(N): all but the N most recent vector memory operations
+// (loads and stores alike; gfx9 reports their completion in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmem_but() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 // Byte offset of logical chunk `chunk` of tile row `r`.
 __device__ __forceinline__ int row_chunk_off(int r, int chunk) {

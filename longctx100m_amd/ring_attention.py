@@ -152,15 +152,31 @@ def bwd_preprocess(out, dout, m, l, delta=None, lse2=None):
 
 def bwd_shard(q, k, v, dout, lse2, delta, *, q_pos0: int, k_pos0: int, causal: bool = True,
               valid_length: Optional[int] = None, dq_acc=None, dk_acc=None, dv_acc=None,
-              precise: bool = False):
-    """One hop of the backward; adds into the fp32 accumulators given."""
+              precise: bool = False, workspace=None):
+    """One hop of the backward; adds into the fp32 accumulators given.
+
+    With ``workspace`` (a CUDA tensor, see :func:`bwd_shard_workspace_bytes`)
+    and all three accumulators, the dK/dV kernel stores dS there and dQ is
+    computed from it instead of recomputing the scores."""
     _check_dev(q, k, v, dout, lse2, delta)
     s = _shape(q, k, precise)
     mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    _lib.check(_lib.load().lc_attn_bwd_shard(s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                             dout.data_ptr(), lse2.data_ptr(), delta.data_ptr(),
-                                             ptr(dq_acc), ptr(dk_acc), ptr(dv_acc), _stream()))
+    args = (s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(), lse2.data_ptr(),
+            delta.data_ptr(), ptr(dq_acc), ptr(dk_acc), ptr(dv_acc))
+    if workspace is None:
+        _lib.check(_lib.load().lc_attn_bwd_shard(*args, _stream()))
+    else:
+        _check_dev(workspace)
+        nbytes = workspace.numel() * workspace.element_size()
+        _lib.check(_lib.load().lc_attn_bwd_shard_ws(*args, workspace.data_ptr(), nbytes,
+                                                    _stream()))
+
+
+def bwd_shard_workspace_bytes(q, k, precise: bool = False) -> int:
+    """Workspace bytes for :func:`bwd_shard` to share dS between its kernels
+    (0 when the shape does not take that path)."""
+    return int(_lib.load().lc_attn_bwd_shard_workspace_bytes(_shape(q, k, precise)))
 
 
 # ------------------------------------------------------- reference signatures --

@@ -202,6 +202,64 @@ def test_bwd_shard_long_stream(ra, gpu, case):
     assert norm_rel(_np(dv), edv) <= BF16_TOL
 
 
+DS_CASES = [
+    # b, nq, nk, hq, hkv, q_pos0, k_pos0, causal, valid, workspace fraction
+    (1, 256, 256, 2, 2, 0, 0, True, None, 1.0),       # diagonal block
+    (1, 300, 200, 4, 2, 500, 100, True, None, 1.0),   # tails, GQA, offsets
+    (2, 200, 333, 2, 1, 100, 0, True, 250, 1.0),      # batch, valid_length, odd key blocks
+    (1, 160, 130, 4, 1, 0, 0, False, None, 1.0),      # non-causal, partial last key block
+    (1, 96, 64, 3, 1, 0, 64, True, None, 1.0),        # rows that see no key
+    (1, 700, 500, 2, 2, 0, 0, True, None, 0.3),       # query chunks of 128 rows
+    (1, 256, 256, 1, 1, 0, 0, True, None, 0.01),      # no usable workspace: recompute path
+    (2, 32, 70000, 1, 1, 69980, 0, True, None, 1.0),  # dQ over key sub-shards of the blocks
+    (1, 70000, 64, 2, 2, 0, 0, True, None, 1.0),      # query chunks of 65,536 rows
+]
+
+
+@pytest.mark.parametrize("case", DS_CASES)
+def test_bwd_shard_shared_ds(ra, gpu, case):
+    """dS sharing (dK/dV stores dS, dQ reads it back): against the oracle at
+    the bf16 bar, dK/dV bit-identical to the recomputing path (same kernel,
+    plus stores) unless the workspace splits the queries into more chunks, dQ
+    equal to it up to the rounding of dS."""
+    b, nq, nk, hq, hkv, qp, kp, causal, valid, frac = case
+    d = 128
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    q = _t(gpu, rng.standard_normal((b, nq, hq, d)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((b, nk, hkv, d)), gpu.bfloat16)
+    do = _t(gpu, rng.standard_normal((b, nq, hq, d)), gpu.bfloat16)
+    kw = dict(q_pos0=qp, k_pos0=kp, causal=causal, valid_length=valid)
+    o32, m, l = ra.fwd_shard(q, k, v, **kw)
+    out = o32.to(gpu.bfloat16)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    full = ra.bwd_shard_workspace_bytes(q, k)
+    assert full == b * hq * -(-min(nq, 65536) // 32) * -(-nk // 32) * 2048
+    # stale non-finite bytes: every block the dQ kernel uses must be written first
+    ws = gpu.full((max(256, int(full * frac)) // 2,), float("nan"), dtype=gpu.bfloat16,
+                  device="cuda")
+    grads = []
+    for w in (ws, None):
+        dq = gpu.zeros((b, nq, hq, d), dtype=gpu.float32, device="cuda")
+        dk = gpu.zeros((b, nk, hkv, d), dtype=gpu.float32, device="cuda")
+        dv = gpu.zeros_like(dk)
+        ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, workspace=w, **kw)
+        grads.append((_np(dq), _np(dk), _np(dv)))
+    gpu.cuda.synchronize()
+    (dq, dk, dv), (rdq, rdk, rdv) = grads
+    tiles = full // (b * hq * -(-nk // 32) * 2048)  # 32-row query tiles of the full workspace
+    chunked = 4 <= int(full * frac) // (full // tiles) < -(-nq // 32)
+    if chunked:  # dK/dV summed chunk by chunk: same terms, another fp32 order
+        assert norm_rel(dk, rdk) <= 1e-5 and norm_rel(dv, rdv) <= 1e-5
+    else:
+        assert np.array_equal(dk, rdk) and np.array_equal(dv, rdv)
+    assert norm_rel(dq, rdq) <= 4e-3
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **kw)
+    assert norm_rel(dq, edq) <= BF16_TOL
+    assert norm_rel(dk, edk) <= BF16_TOL
+    assert norm_rel(dv, edv) <= BF16_TOL
+
+
 def test_merge_is_order_invariant(ra, gpu):
     rng = np.random.default_rng(5)
     nq, hq, d = 192, 2, 128
