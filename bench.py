@@ -6,10 +6,13 @@ Workload (one "step"): rank 7 of an 8-rank ring, a 32768-token bf16 local
 query shard, Hq = Hkv = 16, d = 128.  Forward: the diagonal KV shard plus 7
 preceding full KV shards, each hop's partial merged by log-sum-exp into the
 running state (fwd kernel + merge kernel per hop).  Backward: preprocess
-(delta, LSE), then per hop the dQ kernel (accumulating dQ across shards) and
-the dK/dV kernel (per-shard dK/dV, as they would travel back around the
-ring).  Inputs (Q, K, V, dO ~ N(0,1), seeded) are resident in HBM before the
-timed region.
+(delta, LSE), then per hop the dK/dV kernel (per-shard dK/dV, as they would
+travel back around the ring), which also stores dS (bf16) in a workspace,
+and the dQ kernel that reads it back (accumulating dQ across shards);
+--bwd-recompute runs the dQ kernel that recomputes S and dP instead.
+Inputs (Q, K, V, dO ~ N(0,1), seeded) are resident in HBM before the timed
+region; the dS workspace (34 GiB at the default shape) is allocated before
+it.
 
 FLOP convention (algorithmic, fully masked tiles not counted): a full
 (query shard x KV shard) forward is 4*Nq*Nk*H*d, the diagonal counts half,
@@ -619,7 +622,8 @@ def main() -> int:
             "workload": (f"BASELINE configs 2+3: rank {rank} of {world}, {n}-token bf16 local "
                          f"shard, Hq=Hkv={h}, d={d}; fwd over diagonal + {n_full} full KV shards "
                          f"with LSE merge, then recompute bwd (dQ across shards, dK/dV per "
-                         f"shard)"),
+                         f"shard; " + ("dS shared by the dK/dV and dQ kernels)" if ws is not None
+                                       else "dQ kernel recomputes dS)")),
             "world": world, "rank": rank, "local_tokens": n, "heads_q": h, "heads_kv": h,
             "head_dim": d, "parallelism": "one rank's share on one GPU (ring emulated in HBM)",
         },
