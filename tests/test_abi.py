@@ -129,3 +129,29 @@ def test_last_error_is_per_thread(lib):
     t.join()
     assert seen["msg"] == "block_q and block_k must be positive"
     assert lib.lc_last_error().decode() == "rank 5 out of range for world_size 2"
+
+
+def test_shared_ds_workspace_size_and_errors(lib):
+    """lc_attn_bwd_shard_workspace_bytes: 2 bytes per (query, key, query head) of up to
+    65,536 query rows, in 32 x 32 blocks; 0 off the d=128 bf16 path.  The workspace entry
+    rejects bad arguments before touching the GPU."""
+    bf, f32 = _lib.LC_DTYPE_BF16, _lib.LC_DTYPE_F32
+    size = lambda *s: lib.lc_attn_bwd_shard_workspace_bytes(_lib.Shape(*s))  # noqa: E731
+    assert size(1, 32768, 32768, 16, 16, 128, bf, 0) == 16 * 1024 * 1024 * 2048
+    assert size(2, 100, 70, 4, 2, 128, bf, 0) == 2 * 4 * 4 * 3 * 2048
+    assert size(1, 200000, 64, 1, 1, 128, bf, 0) == 2048 * 2 * 2048  # 65,536-row chunks
+    assert size(1, 256, 256, 2, 2, 64, bf, 0) == 0
+    assert size(1, 256, 256, 2, 2, 128, f32, 0) == 0
+    assert size(1, 256, 256, 2, 2, 128, bf, _lib.LC_FLAG_PRECISE) == 0
+    assert size(1, 256, 256, 3, 2, 128, bf, 0) == 0  # invalid shape
+    shape = _lib.Shape(1, 64, 64, 2, 2, 128, bf, 0)
+    mask = _lib.Mask(0, 0, -1, 1, 0)
+    rc = lib.lc_attn_bwd_shard_ws(shape, mask, None, 16, 16, 16, 16, 16, 16, 16, 16, None, 0,
+                                  None)
+    assert rc == _lib.LC_ERR_INVALID and lib.lc_last_error().decode() == "null pointer argument"
+    rc = lib.lc_attn_bwd_shard_ws(shape, mask, 16, 16, 16, 16, 16, 16, 16, 16, None, None, 0,
+                                  None)
+    assert rc == _lib.LC_ERR_INVALID and "both be set" in lib.lc_last_error().decode()
+    rc = lib.lc_attn_bwd_shard_ws(shape, mask, 16, 16, 16, 16, 16, 16, 16, 16, 16, None, 4096,
+                                  None)
+    assert rc == _lib.LC_ERR_INVALID and "workspace is NULL" in lib.lc_last_error().decode()
