@@ -142,7 +142,7 @@ int lc_attn_bwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
  * workspace and dQ is computed from it, without recomputing the scores.  The
  * workspace holds the dS of a chunk of query rows at a time: the full size
  * from lc_attn_bwd_shard_workspace_bytes runs the pair in chunks of up to
- * 65,536 rows; a smaller one runs smaller chunks (multiples of 128 rows).
+ * 65,536 rows; a smaller one runs smaller chunks (multiples of 256 rows).
  * With no usable workspace, or other shapes, this is lc_attn_bwd_shard.
  * Results agree with lc_attn_bwd_shard up to fp32 summation order. */
 size_t lc_attn_bwd_shard_workspace_bytes(const lc_attn_shape_t* shape);

@@ -200,7 +200,7 @@ int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
 // workspace given): the dK/dV kernel stores the dS it forms and the dQ
 // kernel reads it back, so dQ costs one GEMM instead of three (S, dP and dQ).
 // The workspace holds the dS of one chunk of query rows at a time; chunks are
-// multiples of 128 rows (one dQ workgroup) of at most kStreamChunk rows.
+// multiples of 256 rows (one dQ workgroup) of at most kStreamChunk rows.
 // Returns the chunk's row count, 0 when the shape or workspace does not allow
 // it.
 int64_t ds_chunk_rows(const lc::Problem& p, size_t ws_bytes) {
@@ -209,7 +209,7 @@ int64_t ds_chunk_rows(const lc::Problem& p, size_t ws_bytes) {
   if (per_tile == 0) return 0;
   int64_t rows = (int64_t)(ws_bytes / per_tile) * 32;
   rows = std::min<int64_t>(rows, kStreamChunk);
-  rows = rows >= p.Nq ? p.Nq : rows / 128 * 128;
+  rows = rows >= p.Nq ? p.Nq : rows / 256 * 256;
   // block indices of one chunk are 32-bit in the kernels
   if ((int64_t)p.B * p.Hq * ((rows + 31) / 32) * nkb >= (int64_t)1 << 31) return 0;
   return rows;
