@@ -78,6 +78,16 @@ int lc_rope_apply(int32_t dtype, int64_t tokens, int32_t heads, int32_t head_dim
 int lc_swiglu(int32_t dtype, int64_t rows, int32_t cols, const void* gate, int64_t gate_stride,
               const void* up, int64_t up_stride, void* out, void* stream);
 
+/* One token through a bias-free linear layer, replacing candle's Linear
+ * forward at M = 1 (rust/longctx100m-model/src/model.rs:64-76, the q/k/v/o
+ * projections :99-102, the MLP :290-292) and the LM head matmul (:670-674)
+ * in the decode step:
+ *   y[n] = dtype( sum_k w[n * w_stride + k] * x[k] ),  n < rows, k < cols
+ * with fp32 accumulation.  bf16 only; cols and w_stride multiples of 8,
+ * w_stride >= cols, w and x 16-byte aligned.  For more tokens use a GEMM. */
+int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_stride,
+            const void* x, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

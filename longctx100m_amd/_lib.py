@@ -122,6 +122,8 @@ SIGNATURES = {
                               c_void_p, c_void_p]),
     "lc_swiglu": (c_int, [c_int32, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                           c_void_p, c_void_p]),
+    "lc_gemv": (c_int, [c_int32, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_void_p,
+                        c_void_p]),
     "lc_last_error": (ctypes.c_char_p, []),
     "lc_abi_version": (c_int32, []),
 }

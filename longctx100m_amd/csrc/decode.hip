@@ -25,6 +25,14 @@ namespace {
 
 constexpr int D = 128;
 constexpr int TK = 32;  // keys per tile
+// K/V tiles in LDS per workgroup: the one in use and kStages - 1 in flight.
+// LDS bounds stages x workgroups per CU; measured one C4 layer (262,144 keys,
+// 8 KV heads): 2 stages (5 workgroups per CU) 4.76 TB/s, 3 stages (3 per CU)
+// 5.24 TB/s, 4 and 5 stages (2 per CU) 4.72 and 4.79 TB/s: a lone wave per
+// SIMD cannot hide its own MFMA and LDS latencies.
+constexpr int kStages = 3;
+constexpr int kLdInst = 2 * TK / 4;  // DMA instructions per K+V tile (4 rows each)
+static_assert((kStages - 2) * kLdInst < 64, "vmcnt immediate");
 constexpr int KS = D / 32;
 constexpr int DB = D / 16;
 constexpr int kTileBytes = TK * t128::kRowBytes;
@@ -43,9 +51,21 @@ struct DecodeArgs {
   float sl2;  // scale * log2(e)
 };
 
+// Waits until at most n tiles' loads are outstanding (n < kStages - 1).
+__device__ __forceinline__ void wait_tiles(int n) {
+  static_assert(kStages <= 6, "wait_tiles cases");
+  switch (n) {
+    case 0: t128::wait_vmem(); break;
+    case 1: t128::wait_vmem_but<kLdInst>(); break;
+    case 2: t128::wait_vmem_but<(2 * kLdInst < 64 ? 2 * kLdInst : 0)>(); break;
+    case 3: t128::wait_vmem_but<(3 * kLdInst < 64 ? 3 * kLdInst : 0)>(); break;
+    default: t128::wait_vmem_but<(4 * kLdInst < 64 ? 4 * kLdInst : 0)>(); break;
+  }
+}
+
 __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t kbuf[kStages][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t vbuf[kStages][kTileBytes];
 
   const int lane = threadIdx.x;
   const int c = lane & 15;
@@ -69,10 +89,11 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
 
   t128::RowLoader<TK, 1> ld;
   ld.init(ks, 0, lane);
-  if (ntiles > 0) {
-    ld.load(kbase, ks, (int)kb0, a.Nk, t128::lds_addr(kbuf), 0, lane);
-    ld.load(vbase, ks, (int)kb0, a.Nk, t128::lds_addr(vbuf), 0, lane);
-  }
+  auto issue = [&](int j) {  // tile j into stage j % kStages
+    const int st = j % kStages;
+    ld.load(kbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk, t128::lds_addr(kbuf) + st * kTileBytes, 0, lane);
+    ld.load(vbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk, t128::lds_addr(vbuf) + st * kTileBytes, 0, lane);
+  };
 
   // Row c of this (batch, KV head): query head hk*group + c / Nq, query c % Nq.
   const bool row_ok = c < a.rows;
@@ -89,6 +110,13 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
     }
   }
 
+  // Q is in VGPRs from here on (the compiler, which cannot count the tile
+  // loads below, would otherwise wait for every load before each use of Q).
+  t128::wait_vmem();
+#pragma unroll
+  for (int j = 0; j < kStages - 1; ++j)
+    if (j < ntiles) issue(j);
+
   int koff[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) koff[kk] = t128::row_chunk_off(c, 4 * kk + g);
@@ -103,13 +131,13 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   float lsum = 0.f;        // lane-partial sum of p
 
   for (int j = 0; j < ntiles; ++j) {
-    t128::wait_vmem();
-    if (j + 1 < ntiles) {
-      ld.load(kbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, t128::lds_addr(kbuf) + ((j + 1) & 1) * kTileBytes, 0, lane);
-      ld.load(vbase, ks, (int)(kb0 + (j + 1) * TK), a.Nk, t128::lds_addr(vbuf) + ((j + 1) & 1) * kTileBytes, 0, lane);
-    }
-    const uint8_t* kt = kbuf[j & 1];
-    const uint8_t* vt = vbuf[j & 1];
+    // tiles j + 1 .. j + kStages - 2 (those that exist) may stay in flight
+    wait_tiles(min(kStages - 2, ntiles - 1 - j));
+    // stage (j - 1) % kStages was read by the previous iteration, whose LDS
+    // reads completed before its MFMAs consumed them
+    if (j + kStages - 1 < ntiles) issue(j + kStages - 1);
+    const uint8_t* kt = kbuf[j % kStages];
+    const uint8_t* vt = vbuf[j % kStages];
     const int64_t key0 = kb0 + (int64_t)j * TK;
 
     f32x4 sc[2];
@@ -248,11 +276,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S,
 
 }  // namespace
 
-// Splits per (batch, KV head): enough one-wave workgroups to keep every CU's
-// LDS busy with cache tiles in flight, at least two tiles per split.
+// Splits per (batch, KV head): as many one-wave workgroups as fit the CUs'
+// LDS (kStages tiles each), at least two tiles per split.
 int decode_splits(const Problem& p) {
+  constexpr int kPerCu = (160 * 1024) / (kStages * 2 * kTileBytes);
   const int64_t tiles = ((int64_t)p.Nk + TK - 1) / TK;
-  const int64_t want = (5 * 256 + (int64_t)p.B * p.Hkv - 1) / ((int64_t)p.B * p.Hkv);
+  const int64_t want = (kPerCu * 256 + (int64_t)p.B * p.Hkv - 1) / ((int64_t)p.B * p.Hkv);
   int64_t s = want < 1 ? 1 : want;
   const int64_t max_s = tiles / 2 < 1 ? 1 : tiles / 2;
   if (s > max_s) s = max_s;

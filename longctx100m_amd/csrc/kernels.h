@@ -111,6 +111,10 @@ hipError_t launch_rope_table(const float* inv, int half, float cos_factor, bool 
 hipError_t launch_rope_apply(int dtype, int64_t tokens, int heads, int head_dim,
                              const float* table, const void* src, int64_t sts, void* dst,
                              hipStream_t s);
+// y[n] = bf16(sum_k w[n][k] x[k]) for a bf16 [n, k] row-major w (row stride
+// ws elements), bf16 x [k]; k % 8 == 0, ws % 8 == 0, 16-byte aligned (gemv.hip).
+hipError_t launch_gemv_bf16(int64_t n, int k, const void* w, int64_t ws, const void* x, void* y,
+                            hipStream_t s);
 hipError_t launch_swiglu(int dtype, int64_t rows, int cols, const void* g, int64_t gs,
                          const void* u, int64_t us, void* out, hipStream_t s);
 

@@ -156,4 +156,21 @@ int lc_swiglu(int32_t dtype, int64_t rows, int32_t cols, const void* gate, int64
   return e == hipSuccess ? LC_OK : hip_error(e, "swiglu launch");
 }
 
+int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_stride,
+            const void* x, void* y, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
+  if (dtype != LC_DTYPE_BF16) return set_error(LC_ERR_UNSUPPORTED, "gemv supports bf16 only");
+  if (rows < 0 || cols <= 0 || cols % 8 != 0)
+    return set_error(LC_ERR_INVALID, "gemv needs rows >= 0 and cols > 0, cols %% 8 == 0");
+  if (!w || !x || !y) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (!stride_ok(w_stride, cols))
+    return set_error(LC_ERR_INVALID, "row strides must be >= cols and multiples of 8 elements");
+  if (!aligned16(w) || !aligned16(x))
+    return set_error(LC_ERR_INVALID, "gemv w and x must be 16-byte aligned");
+  if (rows == 0) return LC_OK;
+  hipError_t e = lc::launch_gemv_bf16(rows, cols, w, w_stride, x, y,
+                                      static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "gemv launch");
+}
+
 }  // extern "C"

@@ -175,10 +175,11 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // s_waitcnt vmcnt(N): all but the N most recent vector memory operations
 // (loads and stores alike; gfx9 reports their completion in issue order).
+// vmcnt is 6 bits: 3:0 in bits 3:0 of the immediate, 5:4 in bits 15:14.
 template <int N>
 __device__ __forceinline__ void wait_vmem_but() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // Byte offset of logical chunk `chunk` of tile row `r`.

@@ -1,6 +1,7 @@
 """Decoder-layer prefill share on MI355X: RMSNorm, RoPE and SwiGLU kernels
 (include/longctx100m_layer.h) around the ring attention of this package, with
-the projections as library GEMMs (torch.matmul -> hipBLASLt).
+the projections as library GEMMs (torch.matmul -> hipBLASLt), except one decode token,
+which goes through lc_gemv.
 
 Mirrors the reference's decoder (rust/longctx100m-model/src/model.rs:387-393):
     h = RMSNorm(x); q, k, v = proj(h); q, k = RoPE(q, k); a = attention(q, k, v)
@@ -122,6 +123,26 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
                                      gate.stride(0), up.data_ptr(), up.stride(0),
                                      out.data_ptr(), _stream()))
     return out
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x @ w.T for a bias-free linear layer (candle Linear,
+    rust/longctx100m-model/src/model.rs:64-76).  One bf16 token goes through
+    the bandwidth-bound lc_gemv (the decode step); anything else is a library
+    GEMM."""
+    if (x.dim() == 2 and x.shape[0] == 1 and x.dtype == torch.bfloat16
+            and w.dtype == torch.bfloat16 and x.is_contiguous() and w.stride(1) == 1
+            and w.shape[1] % 8 == 0 and w.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0):
+        _chk_cuda(x, w)
+        rows, cols = w.shape
+        if x.shape[1] != cols:
+            raise ValueError("x and w do not match")
+        y = torch.empty((1, rows), dtype=x.dtype, device=x.device)
+        _lib.check(_lib.load().lc_gemv(_dtype_code(x), rows, cols, w.data_ptr(), w.stride(0),
+                                       x.data_ptr(), y.data_ptr(), _stream()))
+        return y
+    return torch.matmul(x, w.t())
 
 
 # ------------------------------------------------------------- the model --
@@ -258,7 +279,7 @@ def layer_decode(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
     else:
         xin = x
         h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps)
-    qkv = torch.matmul(h, w["wqkv"].t())
+    qkv = linear(h, w["wqkv"])
     trow = table[pos:pos + 1]
     q = rope_apply(qkv[:, :hq * d], trow, hq, d)
     kc, vc = cache
@@ -267,13 +288,13 @@ def layer_decode(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
     o, _, _ = ra.decode(q.view(1, 1, hq, d), kc[:, :pos + 1], vc[:, :pos + 1], q_pos0=pos,
                         k_pos0=0, workspace=workspace)
     attn = o.to(x.dtype).view(1, hq * d)  # the forward output in the model dtype
-    ao = torch.matmul(attn, w["wo"].t())
+    ao = linear(attn, w["wo"])
     x2 = torch.empty_like(x)
     h2 = rmsnorm(xin, w["norm2"], cfg.rms_norm_eps, residual=ao, residual_out=x2)
-    gu = torch.matmul(h2, w["wgu"].t())
+    gu = linear(h2, w["wgu"])
     inter = cfg.intermediate_size
     a = swiglu(gu[:, :inter], gu[:, inter:])
-    return x2, torch.matmul(a, w["wd"].t())
+    return x2, linear(a, w["wd"])
 
 
 def new_cache(cfg: ModelConfig, capacity: int, device, dtype=torch.bfloat16):
@@ -306,7 +327,7 @@ def model_decode_step(token: int, pos: int, weights: Dict, cfg: ModelConfig,
         x, res = layer_decode(x, lw, cfg, table, pos, caches[li], residual=res,
                               workspace=workspace)
     h = rmsnorm(x, weights["final_norm"], cfg.rms_norm_eps, residual=res)
-    return torch.matmul(h, weights["lm_head"].t())
+    return linear(h, weights["lm_head"])
 
 
 def init_model_weights(cfg: ModelConfig, gen: torch.Generator, device, dtype=torch.bfloat16,

@@ -155,3 +155,15 @@ def test_shared_ds_workspace_size_and_errors(lib):
     rc = lib.lc_attn_bwd_shard_ws(shape, mask, 16, 16, 16, 16, 16, 16, 16, 16, 16, None, 4096,
                                   None)
     assert rc == _lib.LC_ERR_INVALID and "workspace is NULL" in lib.lc_last_error().decode()
+
+
+def test_gemv_argument_errors(lib):
+    bf, f32 = _lib.LC_DTYPE_BF16, _lib.LC_DTYPE_F32
+    assert lib.lc_gemv(f32, 4, 8, 16, 8, 16, 16, None) == _lib.LC_ERR_UNSUPPORTED
+    assert lib.lc_gemv(bf, 4, 12, 16, 16, 16, 16, None) == _lib.LC_ERR_INVALID
+    assert lib.lc_gemv(bf, 4, 8, 16, 12, 16, 16, None) == _lib.LC_ERR_INVALID
+    assert lib.lc_gemv(bf, 4, 8, None, 8, 16, 16, None) == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == "null pointer argument"
+    assert lib.lc_gemv(bf, 4, 8, 24, 8, 16, 16, None) == _lib.LC_ERR_INVALID
+    assert "aligned" in lib.lc_last_error().decode()
+    assert lib.lc_gemv(bf, 0, 8, 16, 8, 16, 16, None) == _lib.LC_OK

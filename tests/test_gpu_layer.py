@@ -35,11 +35,16 @@ def _np(t):
     return t.detach().float().cpu().numpy()
 
 
-def _close(got, want, dtype):
+def _close(got, want, dtype, rare=0.0):
+    """bf16: within one ulp; with rare > 0 a fraction <= rare of the elements may
+    be within two (large samples: a sum of squares rounded differently moves
+    h * inv across a rounding boundary, and the second rounding can add to it)."""
     if dtype == "bf16":
         rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-30)
-        bad = (rel > BF16_ULP) & (np.abs(got - want) > 1e-30)
-        assert not bad.any(), (got[bad][:5], want[bad][:5])
+        far = np.abs(got - want) > 1e-30
+        bad = (rel > BF16_ULP) & far
+        assert not ((rel > 2 * BF16_ULP) & far).any(), (got[bad][:5], want[bad][:5])
+        assert bad.mean() <= rare, (bad.sum(), got[bad][:5], want[bad][:5])
     else:
         np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
 
@@ -49,7 +54,8 @@ def _dt(gpu, name):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("rows,cols,with_res", [(37, 4096, False), (64, 1000, True), (5, 16384, True)])
+@pytest.mark.parametrize("rows,cols,with_res", [(37, 4096, False), (64, 1000, True), (5, 16384, True),
+                                                 (2000, 4096, True)])
 def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
     rng = np.random.default_rng(rows * 7 + cols)
     x = rng.standard_normal((rows, cols)).astype(np.float32) * 2
@@ -72,7 +78,7 @@ def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
         out = ly.rmsnorm(xv, tw, 1e-5)
         want, _ = L.rmsnorm(x, w, 1e-5, dtype=dtype)
     gpu.cuda.synchronize()
-    _close(_np(out), want, dtype)
+    _close(_np(out), want, dtype, rare=1e-5 if rows * cols > 1 << 20 else 0.0)
 
 
 @pytest.mark.parametrize("scaling", [None, {"rope_type": "linear", "factor": 4.0},
@@ -201,3 +207,23 @@ def test_decode_steps_match_prefill(ly, gpu):
         logits = ly.model_decode_step(int(ids[pos]), pos, weights, cfg, table, caches)
         gpu.cuda.synchronize()
         assert norm_rel(_np(logits[0]), _np(full[pos])) <= 2e-2, step
+
+
+@pytest.mark.parametrize("rows,cols,stride", [(1000, 512, 512), (33, 4096, 4104), (5, 8, 8),
+                                              (70, 14336, 14336), (129, 1000, 1008)])
+def test_gemv_single_token(ly, gpu, rows, cols, stride):
+    """lc_gemv (one token through a linear layer, bf16, fp32 accumulation)
+    against the fp64 product of the same bf16 values: within one bf16 rounding
+    of the exact value plus the fp32 summation error bound."""
+    rng = np.random.default_rng(rows + cols)
+    w = L.bf16(rng.standard_normal((rows, stride)).astype(np.float32) * 0.05)
+    x = L.bf16(rng.standard_normal((1, cols)).astype(np.float32))
+    tw = _t(gpu, w, gpu.bfloat16)[:, :cols]
+    tx = _t(gpu, x, gpu.bfloat16)
+    got = _np(ly.linear(tx, tw))
+    gpu.cuda.synchronize()
+    prod = w[:, :cols].astype(np.float64) * x[0].astype(np.float64)
+    want = prod.sum(axis=1)[None, :]
+    bound = 2.0 ** -8 * np.abs(want) + 2.0 ** -22 * cols * np.abs(prod).sum(axis=1)[None, :]
+    assert got.shape == (1, rows)
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
