@@ -82,44 +82,59 @@ constexpr int kNormMaxChunks = 32;  // cols <= 64 * 8 * 32 = 16384
 
 template <typename T, int NC>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, float eps,
-                                                      const T* x, int64_t xs, const T* res,
-                                                      int64_t rs, T* res_out, const T* w,
-                                                      T* out, int64_t os) {
+                                                      const T* __restrict__ x, int64_t xs,
+                                                      const T* __restrict__ res, int64_t rs,
+                                                      T* __restrict__ res_out,
+                                                      const T* __restrict__ w,
+                                                      T* __restrict__ out, int64_t os) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nchunk = cols / 8;
+  // All loads of the row are issued, unconditionally (chunks past the row
+  // re-read its last chunk and are zeroed), before the first use, so a row
+  // costs one memory latency rather than one per chunk (a decode step
+  // normalises single rows, where that latency is the whole cost).
   f32x8 v[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) v[i] = load8<T>(x + row * xs + 8 * min(lane + 64 * i, nchunk - 1));
+  if (res != nullptr) {
+    f32x8 r[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) r[i] = load8<T>(res + row * rs + 8 * min(lane + 64 * i, nchunk - 1));
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = rnd<T>(v[i][j] + r[i][j]);  // x + attn(x) in the model dtype
+    if (res_out != nullptr) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunk) store8<T>(res_out + row * xs + 8 * c, v[i]);
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nchunk) {
-      f32x8 h = load8<T>(x + row * xs + 8 * c);
-      if (res != nullptr) {
-        const f32x8 r = load8<T>(res + row * rs + 8 * c);
+    const bool in = lane + 64 * i < nchunk;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = rnd<T>(h[j] + r[j]);  // x + attn(x) in the model dtype
-        if (res_out != nullptr) store8<T>(res_out + row * xs + 8 * c, h);
-      }
-      v[i] = h;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
-    }
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], in ? v[i][j] : 0.f, ss);
   }
   ss = wave_sum(ss);
   // mean(h^2) + eps, then sqrt and reciprocal as two rounded steps (model.rs:57).
   const float inv = 1.0f / __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), eps));
 #pragma unroll
+  for (int i = 0; i < NC; ++i) {  // weight chunk i, then v[i] is done with
+    const int c = lane + 64 * i;
+    const f32x8 wt = load8<T>(w + 8 * min(c, nchunk - 1));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i][j] = rnd<T>(rnd<T>(__fmul_rn(v[i][j], inv)) * wt[j]);
+  }
+#pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = lane + 64 * i;
-    if (c < nchunk) {
-      const f32x8 wt = load8<T>(w + 8 * c);
-      f32x8 o;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = rnd<T>(rnd<T>(__fmul_rn(v[i][j], inv)) * wt[j]);
-      store8<T>(out + row * os + 8 * c, o);
-    }
+    if (c < nchunk) store8<T>(out + row * os + 8 * c, v[i]);
   }
 }
 
