@@ -213,6 +213,8 @@ DS_CASES = [
     (1, 256, 256, 1, 1, 0, 0, True, None, 0.01),      # no usable workspace: recompute path
     (2, 32, 70000, 1, 1, 69980, 0, True, None, 1.0),  # dQ over key sub-shards of the blocks
     (1, 70000, 64, 2, 2, 0, 0, True, None, 1.0),      # query chunks of 65,536 rows
+    (2, 600, 450, 8, 2, 1000, 900, True, 1300, 0.5),  # batch, GQA 4, offsets, valid_length, chunks
+    (1, 300, 70000, 2, 1, 69800, 0, True, None, 1.0),  # GQA with dQ over key sub-shards
 ]
 
 
