@@ -161,15 +161,12 @@ def long_shard(args, torch, ra) -> int:
     q = randn(1, n, h, d)
     k = [randn(1, n, h, d) for _ in range(2)]
     v = [randn(1, n, h, d) for _ in range(2)]
-    f32 = dict(device=dev, dtype=torch.float32)
-    o_run, o_part = torch.empty(1, n, h, d, **f32), torch.empty(1, n, h, d, **f32)
-    m, l, m2, l2 = (torch.empty(1, h, n, **f32) for _ in range(4))
-    out = torch.empty(1, n, h, d, device=dev, dtype=bf)
+    from longctx100m_amd.rank_step import LongShardForward
+
+    lsf = LongShardForward(q, k, v)
 
     def step():
-        ra.fwd_shard(q, k[1], v[1], q_pos0=n, k_pos0=n, o=o_run, m=m, l=l)      # diagonal
-        ra.fwd_shard(q, k[0], v[0], q_pos0=n, k_pos0=0, o=o_part, m=m2, l=l2)   # full
-        ra.merge(o_run, m, l, o_part, m2, l2, out=out)
+        lsf.forward()
 
     steps = max(1, min(args.steps, 2))
     for _ in range(max(0, min(args.warmup, 1))):
@@ -184,7 +181,7 @@ def long_shard(args, torch, ra) -> int:
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     flops = 1.5 * 4.0 * n * n * h * d
-    resident = sum(x.numel() * x.element_size() for x in (q, *k, *v, o_run, o_part, m, l, m2, l2, out))
+    resident = sum(x.numel() * x.element_size() for x in lsf.resident())
     line = {
         "metric": "causal attn fwd TFLOP/s @1M-token bf16 shard (diagonal + 1 full shard)",
         "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -453,6 +450,8 @@ def main() -> int:
     if args.c4_decode:
         return c4_decode(args, torch, ra)
 
+    from longctx100m_amd.rank_step import RankStep
+
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
     n, h, d, world, rank = args.tokens, args.heads, args.head_dim, args.world, args.rank
@@ -465,36 +464,15 @@ def main() -> int:
     dout = randn(1, n, h, d)
     ks = [randn(1, n, h, d) for _ in range(world)]
     vs = [randn(1, n, h, d) for _ in range(world)]
-    q_pos0 = rank * n
-    owners = [(rank - hop) % world for hop in range(world)]
-    owners = [b for b in owners if b * n <= q_pos0 + n - 1]  # fully masked hops skipped
-
-    f32 = dict(device=dev, dtype=torch.float32)
-    o_run = torch.empty(1, n, h, d, **f32)
-    m = torch.empty(1, h, n, **f32)
-    l = torch.empty(1, h, n, **f32)
-    o_part = torch.empty_like(o_run)
-    m_part = torch.empty_like(m)
-    l_part = torch.empty_like(l)
-    out = torch.empty(1, n, h, d, device=dev, dtype=bf)
-    delta = torch.empty_like(m)
-    lse2 = torch.empty_like(m)
-    dq_acc = torch.empty(1, n, h, d, **f32)
-    dk_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
-    dv_acc = {b: torch.empty(1, n, h, d, **f32) for b in owners}
-    ws = None
-    if not args.bwd_recompute:
-        ws_bytes = ra.bwd_shard_workspace_bytes(q, ks[0])
-        if ws_bytes:
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            log(f"dS exchange workspace: {ws_bytes / 2**30:.1f} GiB")
+    rs = RankStep(q, dout, ks, vs, rank, share_ds=not args.bwd_recompute)
+    owners = rs.owners
+    ws = rs.workspace
+    if ws is not None:
+        log(f"dS exchange workspace: {ws.numel() / 2**30:.1f} GiB")
 
     timers = {}
 
     def timed(name, fn):
-        if timers is None or name is None:
-            fn()
-            return
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         fn()
@@ -502,43 +480,7 @@ def main() -> int:
         timers.setdefault(name, []).append((s, e))
 
     def step(record: bool):
-        nonlocal timers
-        saved = timers
-        if not record:
-            timers = None
-        for i, b in enumerate(owners):
-            tag = "diag" if b == rank else "full"
-            if i == 0:
-                timed(f"fwd_{tag}", lambda b=b: ra.fwd_shard(q, ks[b], vs[b], q_pos0=q_pos0,
-                                                             k_pos0=b * n, o=o_run, m=m, l=l))
-            else:
-                timed(f"fwd_{tag}", lambda b=b: ra.fwd_shard(q, ks[b], vs[b], q_pos0=q_pos0,
-                                                             k_pos0=b * n, o=o_part, m=m_part,
-                                                             l=l_part))
-                last = i + 1 == len(owners)
-                timed("merge", lambda last=last: ra.merge(o_run, m, l, o_part, m_part, l_part,
-                                                          out=out if last else None))
-        if len(owners) == 1:
-            ra.cast(o_run, out)
-        timed("bwd_preprocess", lambda: ra.bwd_preprocess(out, dout, m, l, delta, lse2))
-        dq_acc.zero_()
-        for b in owners:
-            dk_acc[b].zero_()
-            dv_acc[b].zero_()
-        for b in owners:
-            tag = "diag" if b == rank else "full"
-            if ws is not None:  # dK/dV stores dS, dQ reads it back
-                timed(f"bwd_{tag}", lambda b=b: ra.bwd_shard(
-                    q, ks[b], vs[b], dout, lse2, delta, q_pos0=q_pos0, k_pos0=b * n,
-                    dq_acc=dq_acc, dk_acc=dk_acc[b], dv_acc=dv_acc[b], workspace=ws))
-                continue
-            timed(f"dq_{tag}", lambda b=b: ra.bwd_shard(q, ks[b], vs[b], dout, lse2, delta,
-                                                        q_pos0=q_pos0, k_pos0=b * n,
-                                                        dq_acc=dq_acc))
-            timed(f"dkdv_{tag}", lambda b=b: ra.bwd_shard(q, ks[b], vs[b], dout, lse2, delta,
-                                                          q_pos0=q_pos0, k_pos0=b * n,
-                                                          dk_acc=dk_acc[b], dv_acc=dv_acc[b]))
-        timers = saved
+        rs.step(timed if record else None)
 
     for i in range(args.warmup):
         step(False)
