@@ -29,7 +29,9 @@ import argparse
 import json
 import math
 import os
+import socket
 import sys
+import threading
 import time
 
 PEAK_BF16_TFLOPS = 2516.6
@@ -71,6 +73,17 @@ def parse():
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
     return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(args, target_s: float):
@@ -117,12 +130,58 @@ def cpu_baseline(args, target_s: float):
         "value": round(flops / t / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": oring.num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"C restatement of the reference algorithm (fp32, block_q=64, block_k=128, "
                    f"two-pass backward), 1 of {args.heads} heads, world {world} rank {rank}, "
                    f"{ns}-token shards, d={d}: fwd+bwd {flops / 1e9:.1f} GFLOP in {t:.2f} s"),
         "seconds": round(t, 3),
     }
+
+
+class ClockSampler:
+    """Samples the GPU's current shader clock (torch.cuda.clock_rate, read
+    through amdsmi) every ``period`` seconds while running, so a bench line
+    records the clock its kernels ran at: MI355X boxes of one pool differ by
+    several percent under these kernels, and every kernel time scales with it.
+    Reports None when the clock cannot be read (no amdsmi access)."""
+
+    def __init__(self, torch, period: float = 0.02):
+        self.torch, self.period = torch, period
+        self.samples = []
+        self._stop = threading.Event()
+        self._thread = None
+
+    def _read(self):
+        try:
+            return float(self.torch.cuda.clock_rate(0))
+        except Exception:  # noqa: BLE001 - best effort: amdsmi may be unavailable
+            return None
+
+    def _loop(self):
+        while not self._stop.wait(self.period):
+            v = self._read()
+            if v is None:
+                return
+            self.samples.append(v)
+
+    def __enter__(self):
+        if self._read() is not None:
+            self._thread = threading.Thread(target=self._loop, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join()
+
+    def summary(self):
+        if not self.samples:
+            return None
+        xs = self.samples
+        return {"mean": round(sum(xs) / len(xs), 1), "min": min(xs), "max": max(xs),
+                "samples": len(xs)}
 
 
 def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
@@ -491,11 +550,12 @@ def main() -> int:
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
-    t_start.record()
-    for i in range(args.steps):
-        step(True)
-    t_end.record()
-    torch.cuda.synchronize()
+    with ClockSampler(torch) as clock:
+        t_start.record()
+        for i in range(args.steps):
+            step(True)
+        t_end.record()
+        torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_total = t_start.elapsed_time(t_end)
     ms_per_step = ms_total / args.steps
@@ -539,13 +599,18 @@ def main() -> int:
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": measured_traffic(rl_kernel, n, h, d), "kernel": rl_kernel,
-                "algorithmic": rl_units}
+                "algorithmic": rl_units, "sclk_mhz": clock.summary(),
+                "box": socket.gethostname()}
 
     cpu = None
     if args.cpu_seconds > 0:
         log("cpu baseline (C restatement of the reference algorithm) ...")
         cpu = cpu_baseline(args, args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['seconds']} s)")
+        # the same restatement on the whole workload of this line, at the sample's rate
+        cpu["extrapolated_full_config_s"] = round(total_flops / (cpu["value"] * 1e12), 1)
+        log(f"cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['seconds']} s) "
+            f"of {cpu['cpu_model']}; full config extrapolated: "
+            f"{cpu['extrapolated_full_config_s']} s")
 
     line = {
         "metric": METRIC,
