@@ -98,6 +98,21 @@ int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, con
                    const void* k, const void* v, float* o, float* m, float* l, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* lc_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split partials live in a file-scope device array of
+ * LC_DECODE_STATIC_SCRATCH_BYTES bytes that each GPU the library runs on
+ * holds until the process ends; the call allocates nothing.  Shapes whose
+ * lc_attn_decode_workspace_bytes exceeds that size are rejected with
+ * LC_ERR_WORKSPACE (use lc_attn_decode).  Every call on one GPU shares its
+ * array, so calls that overlap on one GPU (concurrent streams or threads)
+ * race; calls ordered on a stream do not.  Results equal lc_attn_decode's. */
+#define LC_DECODE_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
+int lc_attn_decode_static(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask,
+                          const void* q, const void* k, const void* v, float* o, float* m,
+                          float* l, void* stream);
+
 /* Log-sum-exp merge of a partial (o_part, m_part, l_part) into the running
  * state (o_run, m_run, l_run), in place -- the carried (m, l, acc) state of
  * the reference's hop loop (rs:195-225).  If out != NULL the merged result is

@@ -23,6 +23,8 @@ LC_ERR_HIP = 2
 LC_ERR_UNSUPPORTED = 3
 LC_ERR_WORKSPACE = 4
 
+LC_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
+
 
 class Shape(ctypes.Structure):
     _fields_ = [
@@ -89,6 +91,8 @@ SIGNATURES = {
     "lc_attn_decode_workspace_bytes": (c_size_t, [_S]),
     "lc_attn_decode": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_void_p]),
+    "lc_attn_decode_static": (c_int, [_S, _M, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_void_p]),
     "lc_attn_merge": (c_int, [_S, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p]),
     "lc_attn_init_state": (c_int, [_S, c_void_p, c_void_p, c_void_p, c_void_p]),

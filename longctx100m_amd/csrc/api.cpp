@@ -385,6 +385,35 @@ int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, con
   return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode launch");
 }
 
+int lc_attn_decode_static(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
+                          const void* k, const void* v, float* o, float* m, float* l,
+                          void* stream) {
+  if (int rc = check_shape(shape)) return rc;
+  if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (mask && mask->valid_length < -1)
+    return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
+  const lc::Problem p = make_problem(shape, mask);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p.Nq == 0) return LC_OK;
+  if (!pair_active(p)) {
+    hipError_t e = lc::launch_init_state(p.B, p.Nq, p.Hq, p.D, o, m, l, st);
+    return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode_static init");
+  }
+  if (!lc::decode_supported(p) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      !aligned16(o))
+    return fwd_shard(p, q, k, v, o, m, l, st);  // the blockwise kernels use no scratch
+  const size_t need = round_up(lc::decode_workspace_bytes(p));
+  if (need > lc::kDecodeStaticScratchBytes)
+    return set_error(LC_ERR_WORKSPACE,
+                     "decode needs %zu bytes of scratch, more than the static maximum of %zu; "
+                     "use lc_attn_decode with a workspace",
+                     need, lc::kDecodeStaticScratchBytes);
+  void* scratch = nullptr;
+  LC_TRY_HIP(lc::decode_static_scratch(&scratch), "lc_attn_decode_static scratch address");
+  hipError_t e = lc::launch_decode128(p, q, k, v, o, m, l, scratch, st);
+  return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode_static launch");
+}
+
 int lc_attn_merge(const lc_attn_shape_t* shape, float* o_run, float* m_run, float* l_run,
                   const float* o_part, const float* m_part, const float* l_part, void* out,
                   void* stream) {

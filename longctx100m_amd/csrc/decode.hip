@@ -18,9 +18,20 @@
 #include "kernels.h"
 #include "tile128.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace lc {
+
+// Workspace of lc_attn_decode_static: split partials of the decode kernel,
+// read back by the merge kernel.  Every partial is written before it is read,
+// so nothing here needs clearing between calls.  Each device holds its own
+// copy from the library's load until the process ends, and every call on a
+// device shares it (calls that overlap on one device race).  Host code never
+// passes `scratch` itself to a kernel: its host-side name is not a device
+// address; decode_static_scratch() returns the device address.
+static __device__ __align__(256) uint8_t scratch[kDecodeStaticScratchBytes];
+
 namespace {
 
 constexpr int D = 128;
@@ -297,6 +308,25 @@ size_t decode_workspace_bytes(const Problem& p) {
   const int64_t rows = (int64_t)p.B * p.Nq * p.Hq;
   const int64_t S = decode_splits(p);
   return (size_t)(S * rows * D * 4 + 2 * S * rows * 4);
+}
+
+hipError_t decode_static_scratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with `dev` current
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_decode128(const Problem& p, const void* q, const void* k, const void* v,

@@ -100,6 +100,11 @@ int decode_splits(const Problem& p);
 size_t decode_workspace_bytes(const Problem& p);
 hipError_t launch_decode128(const Problem& p, const void* q, const void* k, const void* v,
                             float* o, float* m, float* l, void* ws, hipStream_t s);
+// Bytes of decode.hip's file-scope device array that stands in for the
+// workspace of lc_attn_decode_static, and that array's address on the
+// current device (looked up once per device; allocates nothing).
+constexpr size_t kDecodeStaticScratchBytes = size_t(16) << 20;
+hipError_t decode_static_scratch(void** ptr);
 
 // Decoder-layer row kernels (layer.hip).
 hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
