@@ -87,7 +87,8 @@ int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
  * bf16, head_dim 128 and q_tokens * heads_q / heads_kv <= 16 the key range of
  * each (batch, KV head) is split over many one-wave workgroups that stream the
  * cache, and a second kernel merges the splits by log-sum-exp; it needs a
- * workspace of lc_attn_decode_workspace_bytes(shape) bytes.  Other shapes run
+ * 16-byte-aligned workspace of lc_attn_decode_workspace_bytes(shape) bytes
+ * (LC_ERR_WORKSPACE if smaller, LC_ERR_INVALID if misaligned).  Other shapes run
  * the lc_attn_fwd_shard kernels (workspace unused; the size query returns 0).
  * No counterpart in the reference, whose generation loops recompute the whole
  * prefill for every new token (src/longctx100m/distributed_infer.py:185-219,

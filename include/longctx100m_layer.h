@@ -30,12 +30,15 @@ extern "C" {
  *   out = dtype(dtype(h * 1/sqrt(mean(h^2) + eps)) * weight)
  * h is written to residual_out when that pointer is non-NULL: the decoder's
  * residual stream x + attn(x), model.rs:387-393, computed once.  x, residual,
- * residual_out and out are [rows, cols] with row strides in elements; weight
- * is [cols].  cols must be a multiple of 8 and <= 16384. */
+ * residual_out and out are [rows, cols], each with its own row stride in
+ * elements (>= cols, a multiple of 8; residual_out_stride is read only when
+ * residual_out is set); weight is [cols].  cols must be a multiple of 8 and
+ * <= 16384; pointers 16-byte aligned.  (ABI version 2 added
+ * residual_out_stride.) */
 int lc_rmsnorm(int32_t dtype, int64_t rows, int32_t cols, float eps, const void* x,
                int64_t x_stride, const void* residual, int64_t residual_stride,
-               void* residual_out, const void* weight, void* out, int64_t out_stride,
-               void* stream);
+               void* residual_out, int64_t residual_out_stride, const void* weight, void* out,
+               int64_t out_stride, void* stream);
 
 /* RoPE scaling profile (rust/longctx100m-model/src/rope.rs:15-99; config
  * rope_scaling).  type: 0 default, 1 linear, 2 llama3. */

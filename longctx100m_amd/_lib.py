@@ -119,7 +119,7 @@ SIGNATURES = {
                                                    c_int32, c_void_p, c_void_p, c_void_p,
                                                    c_int32, c_int64, c_void_p]),
     "lc_rmsnorm": (c_int, [c_int32, c_int64, c_int32, ctypes.c_float, c_void_p, c_int64, c_void_p,
-                           c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+                           c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
     "lc_rope_inv_freq": (c_int, [POINTER(Rope), c_void_p, c_void_p]),
     "lc_rope_table": (c_int, [POINTER(Rope), c_int64, c_int64, c_void_p, c_void_p]),
     "lc_rope_apply": (c_int, [c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_int64,

@@ -58,6 +58,7 @@ SCRATCH_LIMITS = {
     "dkdv128_kernel": 64,
     "dqds128_kernel": 0,
     "decode128_kernel": 0,
+    "rmsnorm_kernel": 0,
 }
 
 # "Function Name: <kernel>" starts a kernel's block; then "<field> [unit]: value".

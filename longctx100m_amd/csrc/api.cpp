@@ -336,7 +336,7 @@ extern "C" {
 
 const char* lc_last_error(void) { return g_last_error.c_str(); }
 
-int32_t lc_abi_version(void) { return 1; }
+int32_t lc_abi_version(void) { return 2; }
 
 int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
                       const void* k, const void* v, float* o, float* m, float* l, void* stream) {
@@ -381,6 +381,8 @@ int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, con
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(LC_ERR_WORKSPACE, "decode workspace of %zu bytes is smaller than %zu",
                      workspace_bytes, need);
+  if (!aligned16(workspace))  // the split kernel stores 16-byte vectors of partials
+    return set_error(LC_ERR_INVALID, "decode workspace must be 16-byte aligned");
   hipError_t e = lc::launch_decode128(p, q, k, v, o, m, l, workspace, st);
   return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode launch");
 }

@@ -108,8 +108,8 @@ hipError_t decode_static_scratch(void** ptr);
 
 // Decoder-layer row kernels (layer.hip).
 hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
-                          int64_t xs, const void* res, int64_t rs, void* res_out, const void* w,
-                          void* out, int64_t os, hipStream_t s);
+                          int64_t xs, const void* res, int64_t rs, void* res_out, int64_t ros,
+                          const void* w, void* out, int64_t os, hipStream_t s);
 hipError_t launch_rope_table(const float* inv, int half, float cos_factor, bool linear,
                              float pos_scale, int64_t tokens, int64_t pos0, float* table,
                              hipStream_t s);

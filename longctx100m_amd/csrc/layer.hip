@@ -76,32 +76,37 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // ---------------------------------------------------------------- RMSNorm --
-// One wave per row; each lane keeps its 8-element chunks of the row in
-// registers between the sum of squares and the scaling.
-constexpr int kNormMaxChunks = 32;  // cols <= 64 * 8 * 32 = 16384
-
-template <typename T, int NC>
+// WPR waves per row (one for rows of up to 4096 columns, four above); each
+// lane keeps its NC 8-element chunks of the row in registers between the sum
+// of squares and the scaling.  Chunk i of lane l in wave w of the row is
+// chunk (64 w + l) + 64 WPR i of the row.  With at most 8 chunks per lane the
+// row, the residual and the weight chunks fit the registers without spilling.
+template <typename T, int NC, int WPR>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, float eps,
                                                       const T* __restrict__ x, int64_t xs,
                                                       const T* __restrict__ res, int64_t rs,
-                                                      T* __restrict__ res_out,
+                                                      T* __restrict__ res_out, int64_t ros,
                                                       const T* __restrict__ w,
                                                       T* __restrict__ out, int64_t os) {
+  static_assert(4 % WPR == 0, "waves per row divide the workgroup");
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int wave = threadIdx.x >> 6;
+  const int wsub = wave % WPR;  // this wave's part of the row
+  const int64_t row = (int64_t)blockIdx.x * (4 / WPR) + wave / WPR;
+  if (row >= rows) return;  // with WPR > 1 the workgroup holds one row: all or none return
   const int nchunk = cols / 8;
+  const int c0 = 64 * wsub + lane;
   // All loads of the row are issued, unconditionally (chunks past the row
   // re-read its last chunk and are zeroed), before the first use, so a row
   // costs one memory latency rather than one per chunk (a decode step
   // normalises single rows, where that latency is the whole cost).
   f32x8 v[NC];
 #pragma unroll
-  for (int i = 0; i < NC; ++i) v[i] = load8<T>(x + row * xs + 8 * min(lane + 64 * i, nchunk - 1));
+  for (int i = 0; i < NC; ++i) v[i] = load8<T>(x + row * xs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
   if (res != nullptr) {
     f32x8 r[NC];
 #pragma unroll
-    for (int i = 0; i < NC; ++i) r[i] = load8<T>(res + row * rs + 8 * min(lane + 64 * i, nchunk - 1));
+    for (int i = 0; i < NC; ++i) r[i] = load8<T>(res + row * rs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
 #pragma unroll
     for (int i = 0; i < NC; ++i)
 #pragma unroll
@@ -109,52 +114,60 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, fl
     if (res_out != nullptr) {
 #pragma unroll
       for (int i = 0; i < NC; ++i) {
-        const int c = lane + 64 * i;
-        if (c < nchunk) store8<T>(res_out + row * xs + 8 * c, v[i]);
+        const int c = c0 + 64 * WPR * i;
+        if (c < nchunk) store8<T>(res_out + row * ros + 8 * c, v[i]);
       }
     }
   }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const bool in = lane + 64 * i < nchunk;
+    const bool in = c0 + 64 * WPR * i < nchunk;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], in ? v[i][j] : 0.f, ss);
   }
   ss = wave_sum(ss);
+  if constexpr (WPR > 1) {  // the row's waves add their parts in LDS
+    __shared__ float part[4];
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < WPR; ++k) ss += part[k];
+  }
   // mean(h^2) + eps, then sqrt and reciprocal as two rounded steps (model.rs:57).
   const float inv = 1.0f / __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), eps));
 #pragma unroll
   for (int i = 0; i < NC; ++i) {  // weight chunk i, then v[i] is done with
-    const int c = lane + 64 * i;
+    const int c = c0 + 64 * WPR * i;
     const f32x8 wt = load8<T>(w + 8 * min(c, nchunk - 1));
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[i][j] = rnd<T>(rnd<T>(__fmul_rn(v[i][j], inv)) * wt[j]);
   }
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int c = lane + 64 * i;
+    const int c = c0 + 64 * WPR * i;
     if (c < nchunk) store8<T>(out + row * os + 8 * c, v[i]);
   }
 }
 
 template <typename T>
 hipError_t launch_rmsnorm_t(int64_t rows, int cols, float eps, const void* x, int64_t xs,
-                            const void* res, int64_t rs, void* res_out, const void* w, void* out,
-                            int64_t os, hipStream_t s) {
-  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+                            const void* res, int64_t rs, void* res_out, int64_t ros,
+                            const void* w, void* out, int64_t os, hipStream_t s) {
   const int nchunk = cols / 8;
-  auto args = [&](auto kernel) {
+  auto args = [&](auto kernel, int rows_per_block) {
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
     hipLaunchKernelGGL(kernel, grid, block, 0, s, rows, cols, eps, static_cast<const T*>(x), xs,
-                       static_cast<const T*>(res), rs, static_cast<T*>(res_out),
+                       static_cast<const T*>(res), rs, static_cast<T*>(res_out), ros,
                        static_cast<const T*>(w), static_cast<T*>(out), os);
   };
   if (nchunk <= 64 * 2)
-    args(rmsnorm_kernel<T, 2>);
+    args(rmsnorm_kernel<T, 2, 1>, 4);
   else if (nchunk <= 64 * 8)
-    args(rmsnorm_kernel<T, 8>);
-  else
-    args(rmsnorm_kernel<T, kNormMaxChunks>);
+    args(rmsnorm_kernel<T, 8, 1>, 4);
+  else  // up to 64 * 4 * 8 chunks = 16384 columns
+    args(rmsnorm_kernel<T, 8, 4>, 1);
   return hipGetLastError();
 }
 
@@ -241,13 +254,13 @@ unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 }  // namespace
 
 hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,
-                          int64_t xs, const void* res, int64_t rs, void* res_out, const void* w,
-                          void* out, int64_t os, hipStream_t s) {
+                          int64_t xs, const void* res, int64_t rs, void* res_out, int64_t ros,
+                          const void* w, void* out, int64_t os, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  return dtype == 1 ? launch_rmsnorm_t<uint16_t>(rows, cols, eps, x, xs, res, rs, res_out, w, out,
-                                                 os, s)
-                    : launch_rmsnorm_t<float>(rows, cols, eps, x, xs, res, rs, res_out, w, out,
-                                              os, s);
+  return dtype == 1 ? launch_rmsnorm_t<uint16_t>(rows, cols, eps, x, xs, res, rs, res_out, ros, w,
+                                                 out, os, s)
+                    : launch_rmsnorm_t<float>(rows, cols, eps, x, xs, res, rs, res_out, ros, w,
+                                              out, os, s);
 }
 
 hipError_t launch_rope_table(const float* inv, int half, float cos_factor, bool linear,

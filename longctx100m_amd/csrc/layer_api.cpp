@@ -37,8 +37,8 @@ extern "C" {
 
 int lc_rmsnorm(int32_t dtype, int64_t rows, int32_t cols, float eps, const void* x,
                int64_t x_stride, const void* residual, int64_t residual_stride,
-               void* residual_out, const void* weight, void* out, int64_t out_stride,
-               void* stream) {
+               void* residual_out, int64_t residual_out_stride, const void* weight, void* out,
+               int64_t out_stride, void* stream) {
   if (int rc = check_dtype(dtype)) return rc;
   if (rows < 0 || cols <= 0 || cols % 8 != 0 || cols > 16384)
     return set_error(LC_ERR_INVALID, "rmsnorm needs rows >= 0 and 0 < cols <= 16384, cols %% 8 == 0");
@@ -46,15 +46,16 @@ int lc_rmsnorm(int32_t dtype, int64_t rows, int32_t cols, float eps, const void*
   if (residual_out && !residual)
     return set_error(LC_ERR_INVALID, "residual_out needs a residual input");
   if (!stride_ok(x_stride, cols) || !stride_ok(out_stride, cols) ||
-      (residual && !stride_ok(residual_stride, cols)))
+      (residual && !stride_ok(residual_stride, cols)) ||
+      (residual_out && !stride_ok(residual_out_stride, cols)))
     return set_error(LC_ERR_INVALID, "row strides must be >= cols and multiples of 8 elements");
   if (!aligned16(x) || !aligned16(weight) || !aligned16(out) ||
       (residual && !aligned16(residual)) || (residual_out && !aligned16(residual_out)))
     return set_error(LC_ERR_INVALID, "rmsnorm pointers must be 16-byte aligned");
   if (!(eps >= 0.f)) return set_error(LC_ERR_INVALID, "eps must be non-negative");
   hipError_t e = lc::launch_rmsnorm(dtype, rows, cols, eps, x, x_stride, residual,
-                                    residual_stride, residual_out, weight, out, out_stride,
-                                    static_cast<hipStream_t>(stream));
+                                    residual_stride, residual_out, residual_out_stride, weight,
+                                    out, out_stride, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? LC_OK : hip_error(e, "rmsnorm launch");
 }
 

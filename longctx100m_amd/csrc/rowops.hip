@@ -100,26 +100,62 @@ __global__ void cast_kernel(int64_t n, const float* src, T* dst) {
 // delta = rowsum(dout * out) over D (both in the input dtype, upcast to fp32),
 // lse2 = m*log2(e) + log2(max(l, FLT_MIN)), +inf where m = -inf so that
 // 2^(s*log2e - lse2) = 0 for rows that saw no key.  A group of 16 lanes owns
-// one row.
-template <typename T>
-__global__ void bwd_preprocess_kernel(int64_t rows, int N, int H, int D, const T* out,
-                                      const T* dout, const float* m, const float* l, float* delta,
-                                      float* lse2) {
+// a row at a time.  Workgroups walk the [B, N, H, D] rows in memory order
+// (kPreRows consecutive rows each, group g rows g, g + 16, ...), so the reads
+// stream whole DRAM pages; the 4-byte statistics writes land on [B, H, N]
+// lines that the neighbouring workgroups complete in L2.  VEC: elements per
+// 16-byte load (row bytes a multiple of 16, pointers aligned), or 1 for the
+// scalar path.
+constexpr int kPreRows = 64;
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void bwd_preprocess_kernel(int64_t rows, int N, int H, int D,
+                                                             const T* out, const T* dout,
+                                                             const float* m, const float* l,
+                                                             float* delta, float* lse2) {
+  constexpr int kPer = kPreRows / 16;  // rows per lane group
   const int sub = threadIdx.x & 15;
-  const int64_t first = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  const int64_t stride = ((int64_t)gridDim.x * blockDim.x) >> 4;
-  for (int64_t row = first; row < rows; row += stride) {
-    const T* o = out + row * D;
-    const T* g = dout + row * D;
-    float acc = 0.f;
-    for (int d = sub; d < D; d += 16) acc += load_f32(o + d) * load_f32(g + d);
+  const int g = threadIdx.x >> 4;
+  const int64_t r0 = (int64_t)blockIdx.x * kPreRows + g;
+  float acc[kPer];
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (sub == 0) {
+  for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
+  if constexpr (VEC == 1) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t row = min(r0 + 16 * i, rows - 1);
+      for (int d = sub; d < D; d += 16) acc[i] += load_f32(out + row * D + d) * load_f32(dout + row * D + d);
+    }
+  } else {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const int nc = D / VEC;  // 16-byte chunks per row
+    for (int c = sub; c < nc; c += 16) {
+      u32x4 ov[kPer], gv[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {  // every load of the pass issued before use
+        const int64_t off = min(r0 + 16 * i, rows - 1) * D + (int64_t)c * VEC;
+        ov[i] = *reinterpret_cast<const u32x4*>(out + off);
+        gv[i] = *reinterpret_cast<const u32x4*>(dout + off);
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const T* oe = reinterpret_cast<const T*>(&ov[i]);
+        const T* ge = reinterpret_cast<const T*>(&gv[i]);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[i] += load_f32(oe + j) * load_f32(ge + j);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) acc[i] += __shfl_xor(acc[i], off, 64);
+    const int64_t row = r0 + 16 * i;
+    if (sub == 0 && row < rows) {
       const int64_t si = stat_index(row, N, H);
       const float mi = m[si];
       const float li = l[si];
-      delta[si] = acc;
+      delta[si] = acc[i];
       lse2[si] = (mi == -INFINITY) ? INFINITY : mi * kLog2e + log2f(li > kFltMin ? li : kFltMin);
     }
   }
@@ -179,15 +215,28 @@ hipError_t launch_bwd_preprocess(int B, int N, int H, int D, int dtype, const vo
                                  const void* dout, const float* m, const float* l, float* delta,
                                  float* lse2, hipStream_t s) {
   const int64_t rows = (int64_t)B * N * H;
-  const dim3 grid = grid_for(rows * 16);
-  if (dtype == 1)
-    hipLaunchKernelGGL(bwd_preprocess_kernel<uint16_t>, grid, dim3(256), 0, s, rows, N, H, D,
-                       static_cast<const uint16_t*>(out), static_cast<const uint16_t*>(dout), m, l,
-                       delta, lse2);
-  else
-    hipLaunchKernelGGL(bwd_preprocess_kernel<float>, grid, dim3(256), 0, s, rows, N, H, D,
-                       static_cast<const float*>(out), static_cast<const float*>(dout), m, l,
-                       delta, lse2);
+  if (rows == 0) return hipSuccess;
+  const dim3 grid((unsigned)((rows + kPreRows - 1) / kPreRows)), block(256);
+  const bool vec = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(dout)) & 15) == 0;
+  if (dtype == 1) {
+    const uint16_t* o = static_cast<const uint16_t*>(out);
+    const uint16_t* g = static_cast<const uint16_t*>(dout);
+    if (vec && D % 8 == 0)
+      hipLaunchKernelGGL((bwd_preprocess_kernel<uint16_t, 8>), grid, block, 0, s, rows, N, H, D, o,
+                         g, m, l, delta, lse2);
+    else
+      hipLaunchKernelGGL((bwd_preprocess_kernel<uint16_t, 1>), grid, block, 0, s, rows, N, H, D, o,
+                         g, m, l, delta, lse2);
+  } else {
+    const float* o = static_cast<const float*>(out);
+    const float* g = static_cast<const float*>(dout);
+    if (vec && D % 4 == 0)
+      hipLaunchKernelGGL((bwd_preprocess_kernel<float, 4>), grid, block, 0, s, rows, N, H, D, o, g,
+                         m, l, delta, lse2);
+    else
+      hipLaunchKernelGGL((bwd_preprocess_kernel<float, 1>), grid, block, 0, s, rows, N, H, D, o, g,
+                         m, l, delta, lse2);
+  }
   return hipGetLastError();
 }
 

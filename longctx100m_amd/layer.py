@@ -46,13 +46,13 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     out = torch.empty(x2.shape, dtype=x.dtype, device=x.device) if out is None else out
     r2 = residual.reshape(-1, cols) if residual is not None else None
     ro = residual_out.reshape(-1, cols) if residual_out is not None else None
-    if ro is not None and ro.stride(0) != x2.stride(0):
-        raise ValueError("residual_out must share x's row stride")
+    if ro is not None and ro.stride(-1) != 1:
+        raise ValueError("rows must be contiguous")
     _lib.check(_lib.load().lc_rmsnorm(
         _dtype_code(x), x2.shape[0], cols, float(eps), x2.data_ptr(), x2.stride(0),
         r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
-        ro.data_ptr() if ro is not None else None, weight.data_ptr(), out.data_ptr(),
-        out.reshape(-1, cols).stride(0), _stream()))
+        ro.data_ptr() if ro is not None else None, ro.stride(0) if ro is not None else 0,
+        weight.data_ptr(), out.data_ptr(), out.reshape(-1, cols).stride(0), _stream()))
     return out.reshape(x.shape)
 
 

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(lib):
     assert sorted(_lib.SIGNATURES) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.lc_abi_version() == 1
+    assert lib.lc_abi_version() == 2
 
 
 def test_struct_layouts_match_header():
@@ -167,3 +167,29 @@ def test_gemv_argument_errors(lib):
     assert lib.lc_gemv(bf, 4, 8, 24, 8, 16, 16, None) == _lib.LC_ERR_INVALID
     assert "aligned" in lib.lc_last_error().decode()
     assert lib.lc_gemv(bf, 0, 8, 16, 8, 16, 16, None) == _lib.LC_OK
+
+
+def test_decode_workspace_checks(lib):
+    """lc_attn_decode rejects a short or misaligned workspace before any device
+    work (the split kernel stores 16-byte vectors of partials)."""
+    s = _lib.Shape(1, 1, 4096, 32, 8, 128, _lib.LC_DTYPE_BF16, 0)
+    mk = _lib.Mask(4095, 0, -1, 1, 0)
+    need = lib.lc_attn_decode_workspace_bytes(ctypes.byref(s))
+    assert need > 0 and need % 256 == 0
+    fake = 1 << 20  # never dereferenced
+    rc = lib.lc_attn_decode(ctypes.byref(s), ctypes.byref(mk), fake, fake, fake, fake, fake, fake,
+                            fake, need - 256, None)
+    assert rc == _lib.LC_ERR_WORKSPACE and "smaller than" in lib.lc_last_error().decode()
+    rc = lib.lc_attn_decode(ctypes.byref(s), ctypes.byref(mk), fake, fake, fake, fake, fake, fake,
+                            fake + 8, need, None)
+    assert rc == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == "decode workspace must be 16-byte aligned"
+
+
+def test_rmsnorm_residual_out_stride_checked(lib):
+    """residual_out has its own row stride (ABI version 2), validated like the others."""
+    fake = 1 << 20
+    rc = lib.lc_rmsnorm(_lib.LC_DTYPE_BF16, 4, 64, 1e-5, fake, 64, fake, 64, fake, 60, fake,
+                        fake, 64, None)
+    assert rc == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == "row strides must be >= cols and multiples of 8 elements"

@@ -55,7 +55,8 @@ def _dt(gpu, name):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rows,cols,with_res", [(37, 4096, False), (64, 1000, True), (5, 16384, True),
-                                                 (2000, 4096, True)])
+                                                 (2000, 4096, True), (3, 6000, True),
+                                                 (9, 16384, False)])
 def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
     rng = np.random.default_rng(rows * 7 + cols)
     x = rng.standard_normal((rows, cols)).astype(np.float32) * 2
@@ -70,10 +71,12 @@ def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
     tw = _t(gpu, w, tdt)
     if with_res:
         tr = _t(gpu, r, tdt)
-        hout = gpu.empty_like(xbig)
-        out = ly.rmsnorm(xv, tw, 1e-5, residual=tr, residual_out=hout[:, :cols])
+        # residual_out contiguous while x is strided: each operand uses its own row stride
+        hout = gpu.full((rows + 1, cols), 7.0, dtype=tdt, device="cuda")
+        out = ly.rmsnorm(xv, tw, 1e-5, residual=tr, residual_out=hout[:rows])
         want, h = L.rmsnorm(x, w, 1e-5, residual=r, dtype=dtype)
-        np.testing.assert_array_equal(_np(hout[:, :cols]), h)
+        np.testing.assert_array_equal(_np(hout[:rows]), h)
+        assert (_np(hout[rows]) == 7.0).all()  # nothing written past the last row
     else:
         out = ly.rmsnorm(xv, tw, 1e-5)
         want, _ = L.rmsnorm(x, w, 1e-5, dtype=dtype)

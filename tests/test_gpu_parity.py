@@ -160,11 +160,70 @@ def test_bwd_shard(ra, gpu, case, dtype_name, precise):
     gpu.cuda.synchronize()
     edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **kw)
     tol = FP32_TOL if (dtype_name == "float32" or precise) else BF16_TOL
-    if dtype_name == "float32":
-        tol = 2e-5  # fp32 reductions over ~300 terms; the reference's own bar is 1e-4 abs
     assert norm_rel(_np(dq), edq) <= tol
     assert norm_rel(_np(dk), edk) <= tol
     assert norm_rel(_np(dv), edv) <= tol
+
+
+FP32_LONG_CASES = [
+    # nq, nk, hq, hkv, d, q_pos0, k_pos0, causal: longer fp32 reductions (dQ over up to
+    # 8192 keys, dK/dV over up to 4096 queries x a GQA group of 2)
+    (128, 8192, 2, 2, 64, 8100, 0, True),
+    (4096, 256, 2, 1, 128, 0, 0, False),
+    (1024, 1536, 2, 1, 96, 600, 0, True),
+]
+
+
+@pytest.mark.parametrize("case", FP32_LONG_CASES)
+def test_bwd_shard_fp32_long(ra, gpu, case):
+    """The fp32 path keeps the 1e-5 bar as the reductions grow (the generic
+    kernels' fp32 sums stay near 1e-6 of the fp64 dense closed form)."""
+    nq, nk, hq, hkv, d, qp, kp, causal = case
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    f32 = gpu.float32
+    q = _t(gpu, rng.standard_normal((1, nq, hq, d)), f32)
+    k = _t(gpu, rng.standard_normal((1, nk, hkv, d)), f32)
+    v = _t(gpu, rng.standard_normal((1, nk, hkv, d)), f32)
+    do = _t(gpu, rng.standard_normal((1, nq, hq, d)), f32)
+    kw = dict(q_pos0=qp, k_pos0=kp, causal=causal)
+    out, m, l = ra.fwd_shard(q, k, v, **kw)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    dq = gpu.zeros((1, nq, hq, d), dtype=f32, device="cuda")
+    dk = gpu.zeros((1, nk, hkv, d), dtype=f32, device="cuda")
+    dv = gpu.zeros_like(dk)
+    ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, **kw)
+    gpu.cuda.synchronize()
+    eo = dense.attention_fwd(_np(q), _np(k), _np(v), **kw)[0]
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **kw)
+    errs = [norm_rel(_np(out), eo), norm_rel(_np(dq), edq), norm_rel(_np(dk), edk),
+            norm_rel(_np(dv), edv)]
+    assert max(errs) <= FP32_TOL, errs
+
+
+@pytest.mark.parametrize("dtype_name,b,n,h,d", [("bfloat16", 2, 300, 3, 128), ("float32", 1, 77, 2, 64),
+                                                ("bfloat16", 1, 50, 4, 36), ("float32", 1, 33, 1, 30)])
+def test_bwd_preprocess(ra, gpu, dtype_name, b, n, h, d):
+    """delta = rowsum(dO * O) in fp32 from the given dtype and lse2 = m log2(e) +
+    log2(max(l, FLT_MIN)), +inf for rows without a key (ring_attention.py:314,
+    rs:382; the 16-byte-load path for d*size % 16 == 0, the scalar path else)."""
+    dtype = getattr(gpu, dtype_name)
+    rng = np.random.default_rng(zlib.crc32(repr((dtype_name, b, n, h, d)).encode()))
+    out = _t(gpu, rng.standard_normal((b, n, h, d)), dtype)
+    do = _t(gpu, rng.standard_normal((b, n, h, d)), dtype)
+    m = rng.standard_normal((b, h, n)).astype(np.float32)
+    l = (1 + 50 * rng.random((b, h, n))).astype(np.float32)
+    m[0, 0, :3] = -np.inf
+    l[0, 0, :3] = 0.0
+    l[0, -1, 5] = 0.0  # clamped to FLT_MIN
+    delta, lse2 = ra.bwd_preprocess(out, do, _t(gpu, m, gpu.float32), _t(gpu, l, gpu.float32))
+    gpu.cuda.synchronize()
+    want = np.einsum("bnhd,bnhd->bhn", _np(out).astype(np.float64), _np(do).astype(np.float64))
+    assert norm_rel(_np(delta), want) <= 1e-6
+    fin = np.isfinite(m)
+    wl = m.astype(np.float64) * np.log2(np.e) + np.log2(np.maximum(l, 1.17549435e-38))
+    got = _np(lse2)
+    assert np.all(np.isposinf(got[~fin]))
+    assert np.abs(got[fin] - wl[fin]).max() <= 2e-6 * max(1.0, np.abs(wl[fin]).max())
 
 
 LONG_BWD_CASES = [
