@@ -66,6 +66,10 @@ def parse():
                     help="BASELINE config 5 instead: forward of a 1,000,000-token bf16 shard "
                          "against its diagonal block plus one full incoming 1M-token KV shard; "
                          "prints its own JSON line with TFLOP/s and the HBM footprint")
+    ap.add_argument("--host-path", action="store_true",
+                    help="time the host-pointer entry points (lc_ring_*_host: the reference's "
+                         "CPU-tensor signatures, PCIe copies included) against the same ring "
+                         "entry points on device-resident shards, at configs 2/3")
     ap.add_argument("--bwd-recompute", action="store_true",
                     help="backward without dS sharing: the dQ kernel recomputes S and dP "
                          "instead of reading the dS the dK/dV kernel stored")
@@ -253,6 +257,94 @@ def long_shard(args, torch, ra) -> int:
         "flops_per_step": flops,
         "hbm_footprint_gb": {"resident_tensors": round(resident / 1e9, 3),
                              "torch_peak_allocated": round(torch.cuda.max_memory_allocated() / 1e9, 3)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def host_path(args, torch, ra) -> int:
+    """The reference's signatures on host memory (lc_ring_fwd_with_stats_host,
+    lc_ring_bwd_host: every call copies all ranks' shards to HBM and the
+    results back) against lc_ring_fwd_with_stats / lc_ring_bwd on the same
+    shards already in HBM, rank 7 of 8, 32,768-token bf16 shards, 16/16 heads,
+    d = 128.  Both run the same kernels; the difference is the PCIe traffic."""
+    import ctypes
+
+    import numpy as np
+
+    from longctx100m_amd import _lib
+
+    n, h, d, world, rank = args.tokens, args.heads, args.head_dim, args.world, args.rank
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(97)
+    bf = torch.bfloat16
+    randn = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(bf)  # noqa: E731
+    log(f"host path: world={world} rank={rank} n={n} H={h} d={d} bf16")
+    qs = [randn(1, n, h, d) for _ in range(world)]
+    ks = [randn(1, n, h, d) for _ in range(world)]
+    vs = [randn(1, n, h, d) for _ in range(world)]
+    gos = [randn(1, n, h, d) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    out, m, l = ra.ring_causal_attention_forward_with_stats(shards, rank)
+    outs, ms, ls = [out] * world, [m] * world, [l] * world
+    torch.cuda.synchronize()
+    host = lambda t: np.ascontiguousarray(t.cpu().view(torch.int16).numpy())  # noqa: E731
+    hq, hk, hv, hg = ([host(t) for t in ts] for ts in (qs, ks, vs, gos))
+    ho, hm, hl = host(out), np.ascontiguousarray(m.cpu().numpy()), np.ascontiguousarray(l.cpu().numpy())
+    desc = _lib.RingDesc(world, rank, 1, n, h, h, d, _lib.LC_DTYPE_BF16, 0, 1, 64, 128, -1, -1)
+    lib = _lib.load()
+    ptrs = lambda arrs: _lib.ptr_array([a.ctypes.data for a in arrs])  # noqa: E731
+    P = [ptrs(x) for x in (hq, hk, hv, [ho] * world, [hm] * world, [hl] * world, hg)]
+    o_h = np.empty_like(ho)
+    m_h, l_h = np.empty_like(hm), np.empty_like(hl)
+    dq_h, dk_h, dv_h = np.empty_like(ho), np.empty_like(ho), np.empty_like(ho)
+
+    def fwd_host():
+        _lib.check(lib.lc_ring_fwd_with_stats_host(ctypes.byref(desc), P[0][0], P[1][0], P[2][0],
+                                                   o_h.ctypes.data, m_h.ctypes.data,
+                                                   l_h.ctypes.data))
+
+    def bwd_host():
+        _lib.check(lib.lc_ring_bwd_host(ctypes.byref(desc), *[x[0] for x in P], dq_h.ctypes.data,
+                                        dk_h.ctypes.data, dv_h.ctypes.data))
+
+    def fwd_dev():
+        ra.ring_causal_attention_forward_with_stats(shards, rank)
+
+    def bwd_dev():
+        ra.ring_causal_attention_backward(shards, rank, outs, ms, ls, gos)
+
+    def wall(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    reps = max(1, min(args.steps, 3))
+    res = {"fwd_host_s": wall(fwd_host, reps), "fwd_device_s": wall(fwd_dev, reps),
+           "bwd_host_s": wall(bwd_host, reps), "bwd_device_s": wall(bwd_dev, reps)}
+    shard = n * h * d * 2
+    stat = h * n * 4
+    fwd_bytes = (1 + 2 * world) * shard + shard + 2 * stat      # Q + all K, V in; out, m, l back
+    bwd_bytes = world * (5 * shard + 2 * stat) + 3 * shard      # q, k, v, out, dO, m, l per rank in; dq, dk, dv back
+    line = {
+        "metric": "host-pointer ring entry points (PCIe-inclusive) vs device-resident, seconds per call",
+        "unit": "s", "n_gpus": 1, "higher_is_better": False, "dtype": "bf16",
+        "data": "synthetic: Q, K, V, dO ~ N(0,1), seeded; host copies in pageable memory",
+        "config": {"workload": f"BASELINE configs 2/3 shapes through the reference signatures: "
+                               f"rank {rank} of {world}, {n}-token shards, Hq=Hkv={h}, d={d}",
+                   "note": "ring_causal_attention_backward returns this rank's dq, dk, dv "
+                           "(rs:281-475): dQ over all 8 hops, dK/dV of its own shard"},
+        **{k: round(v, 4) for k, v in res.items()},
+        "bytes_copied": {"fwd": fwd_bytes, "bwd": bwd_bytes},
+        "effective_copy_GB_per_s": {
+            "fwd": round(fwd_bytes / max(res["fwd_host_s"] - res["fwd_device_s"], 1e-9) / 1e9, 1),
+            "bwd": round(bwd_bytes / max(res["bwd_host_s"] - res["bwd_device_s"], 1e-9) / 1e9, 1)},
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -502,6 +594,8 @@ def main() -> int:
 
     if args.long_shard:
         return long_shard(args, torch, ra)
+    if args.host_path:
+        return host_path(args, torch, ra)
     if args.c4_prefill:
         return c4_prefill(args, torch, ra)
     if args.c4_model:
