@@ -49,12 +49,15 @@ class RankStep:
 
     ``q`` and ``dout`` are this rank's [B, n, Hq, D] bf16 query shard and
     upstream gradient; ``ks``/``vs`` every rank's [B, n, Hkv, D] KV shards in
-    rank order.  After :meth:`forward`, ``out``/``m``/``l`` hold the rank's
-    output and statistics; after :meth:`backward`, ``dq_acc`` holds dQ and
-    ``dk_acc[b]``/``dv_acc[b]`` owner b's dK/dV contribution (fp32)."""
+    rank order.  ``workspace_bytes`` caps the dS workspace (default: the full
+    size, ``lc_attn_bwd_shard_workspace_bytes``).  After :meth:`forward`,
+    ``out``/``m``/``l`` hold the rank's output and statistics; after
+    :meth:`backward`, ``dq_acc`` holds dQ and ``dk_acc[b]``/``dv_acc[b]`` owner
+    b's dK/dV contribution (fp32)."""
 
     def __init__(self, q: torch.Tensor, dout: torch.Tensor, ks: Sequence[torch.Tensor],
-                 vs: Sequence[torch.Tensor], rank: int, *, share_ds: bool = True):
+                 vs: Sequence[torch.Tensor], rank: int, *, share_ds: bool = True,
+                 workspace_bytes: Optional[int] = None):
         self.q, self.dout, self.ks, self.vs, self.rank = q, dout, list(ks), list(vs), rank
         b, n, h, d = q.shape
         self.n = n
@@ -79,7 +82,11 @@ class RankStep:
                                                 for o in self.owners}
         self.workspace: Optional[torch.Tensor] = None
         if share_ds:
+            # the full size holds the dS of up to 65,536 query rows; a smaller workspace runs
+            # each hop's pair in query chunks of multiples of 256 rows
             nbytes = ra.bwd_shard_workspace_bytes(q, self.ks[0])
+            if nbytes and workspace_bytes is not None:
+                nbytes = min(nbytes, workspace_bytes)
             if nbytes:
                 self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
 

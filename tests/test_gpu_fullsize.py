@@ -10,6 +10,10 @@ bench.py times (longctx100m_amd.rank_step).
   key of every owner), following ring_attention.rs:139-233 (forward) and
   :367-460 (backward: P = exp(s - m) / l, dS = P (dO V^T - delta), delta from
   the bf16-cast output, ring_attention.py:314).
+* The config-4 model's attention share: 65,536-token shards, GQA Hq = 32 /
+  Hkv = 8, rank 3 of 4, forward and backward through the same step with a
+  16 GiB dS workspace (query chunks; the full one would be 275 GB), one KV
+  head and its 4 query heads checked in full (dK/dV summed over the group).
 * a 1,000,000-token bf16 shard at rank 1 of 2 (diagonal +
   one full 1M-token KV shard), forward with LSE merge; sampled rows of two
   heads against an fp32 recompute over all visible keys, including the rows
@@ -174,4 +178,72 @@ def test_c5_long_shard_full_size(gpu):
         del kall, vall
     assert torch.isfinite(lsf.out.float()).all()
     del lsf
+    torch.cuda.empty_cache()
+
+
+def _gqa_head_reference(torch, q, kall, vall, dout, q_pos0, scale, chunk=1024):
+    """_head_reference over the query heads of one GQA group: q, dout [n, g, d];
+    kall, vall [N, d] (the group's KV head).  Returns out, m, l, dq [n, g, ...]
+    and dk, dv [N, d] summed over the group (model.rs:85-94 expands K/V with
+    repeat_interleave, so the gradient of a KV head is its group's sum)."""
+    outs, ms, ls, dqs = [], [], [], []
+    dk = dv = None
+    for j in range(q.shape[1]):
+        o, m, l, dq, k_, v_ = _head_reference(torch, q[:, j], kall, vall, dout[:, j], q_pos0,
+                                              scale, chunk)
+        outs.append(o), ms.append(m), ls.append(l), dqs.append(dq)
+        dk = k_ if dk is None else dk + k_
+        dv = v_ if dv is None else dv + v_
+    st = lambda xs: torch.stack(xs, 1)  # noqa: E731
+    return st(outs), st(ms), st(ls), st(dqs), dk, dv
+
+
+def test_c4_attention_share_full_size_gqa_chunked(gpu):
+    """The config-4 model's attention share at its real shape (65,536-token
+    shards, GQA Hq=32 / Hkv=8, d=128, rank 3 of 4: diagonal + 3 full hops)
+    through the bench's step with a 16 GiB dS workspace, so every hop's pair
+    runs in query chunks (the full workspace would be 275 GB).  KV head 5 and
+    its 4 query heads are checked in full: output and statistics of every row,
+    dQ of every row, dK/dV of every key of every owner (summed over the group)."""
+    torch = gpu
+    from longctx100m_amd.rank_step import RankStep
+
+    world, rank, n, hq, hkv, d = 4, 3, 65536, 32, 8, 128
+    g = hq // hkv
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2468)
+    rnd = lambda *s: torch.randn(*s, generator=gen, device=dev).to(torch.bfloat16)  # noqa: E731
+    q = rnd(1, n, hq, d)
+    dout = rnd(1, n, hq, d)
+    ks = [rnd(1, n, hkv, d) for _ in range(world)]
+    vs = [rnd(1, n, hkv, d) for _ in range(world)]
+    rs = RankStep(q, dout, ks, vs, rank, share_ds=True, workspace_bytes=16 << 30)
+    assert rs.owners == [3, 2, 1, 0]
+    assert rs.workspace is not None and rs.workspace.numel() == 16 << 30
+    print(f"fullsize C4 share: n={n} Hq={hq} Hkv={hkv} rank {rank} of {world}, "
+          f"dS workspace 16 GiB (query chunks)", flush=True)
+    rs.step()
+    torch.cuda.synchronize()
+
+    kvh = 5
+    heads = list(range(kvh * g, (kvh + 1) * g))
+    kall = torch.cat([x[0, :, kvh] for x in ks], 0).float()
+    vall = torch.cat([x[0, :, kvh] for x in vs], 0).float()
+    eo, em, el, edq, edk, edv = _gqa_head_reference(
+        torch, q[0, :, heads].float(), kall, vall, dout[0, :, heads].float(), rank * n, d ** -0.5)
+    errs = {
+        "out": _nrel(rs.out[0, :, heads].float(), eo),
+        "dq": _nrel(rs.dq_acc[0, :, heads], edq),
+        "m": float(((rs.m[0, heads].t() - em).abs() / em.abs().clamp(min=1.0)).max()),
+        "l": float(((rs.l[0, heads].t() - el).abs() / el).max()),
+    }
+    for b in rs.owners:
+        errs[f"dk{b}"] = _nrel(rs.dk_acc[b][0, :, kvh], edk[b * n:(b + 1) * n])
+        errs[f"dv{b}"] = _nrel(rs.dv_acc[b][0, :, kvh], edv[b * n:(b + 1) * n])
+    print("fullsize C4 share KV head 5: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+          flush=True)
+    bad = {k: v for k, v in errs.items() if not v <= {"m": 1e-4, "l": 1e-3}.get(k, BF16_TOL)}
+    assert not bad, bad
+    del rs
     torch.cuda.empty_cache()
