@@ -16,8 +16,9 @@
 //             dQ^T += K^T dS^T             (A = K^T: ds_read_b64_tr_b16)
 //   dkdv128 KV-stationary, 4 waves x 32 keys of one KV head, walking every
 //           query head of the GQA group (group sum in registers).  K^T in
-//           VGPRs, the workgroup's V rows in LDS; 32-query tiles of Q, dO,
-//           LSE and delta double-buffered in LDS.
+//           VGPRs, the workgroup's V rows in LDS (negated once, so that
+//           the dP accumulator runs from delta to delta - dP); 32-query
+//           tiles of Q, dO, LSE and delta double-buffered in LDS.
 //             S = Q K^T, dP = dO V^T       (A = Q, dO rows)
 //             dV^T += dO^T P, dK^T += Q^T dS  (A = dO^T, Q^T: transposed reads)
 // and, when one caller wants dQ and dK/dV of the same shard pair and gives a
@@ -528,6 +529,19 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   // pending) would wait for the K loads before each S step, i.e. for every
   // load and store issued before that point.
   t128::wait_vmem();
+  // V enters dP = dO V^T negated, so that the dP accumulator can start at
+  // delta and end at delta - dP: dS = P (dP - delta) = -(P (delta - dP)).
+  // Each wave negates the 32 rows it reads (written by every wave's DMA).
+  __syncthreads();
+  {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    uint8_t* vw = v_lds + wave * kKvKW * t128::kRowBytes + lane * 16;
+#pragma unroll
+    for (int i = 0; i < kKvKW * t128::kRowBytes / 1024; ++i) {
+      u32x4* p = reinterpret_cast<u32x4*>(vw + i * 1024);
+      *p = *p ^ 0x80008000u;
+    }
+  }
 
   // Row l%32 of a Q/dO tile, dims 16t + 8h .. +7, is roff0 ^ (32 t); the
   // wave's V rows are the same offsets in the wave's part of the V tile.
@@ -544,20 +558,25 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   // One query tile as a stream of 32 MFMA steps j, each with its operands
   // fetched from LDS two steps ahead (A[j&1], B[j&1]):
   //   j  0- 7  S    += Q[:, 16t..]  K^T            (t = j)
-  //   j  8-15  dP   += dO[:, 16t..] V^T            (t = j - 8)
+  //   j  8-15  E    += dO[:, 16t..] (-V)^T         (t = j - 8), E = delta at j = 8
   //   j 16-23  dV^T += dO^T P       (u, dblk) = ((j-16)/4, (j-16)%4)
   //   j 24-31  dK^T += Q^T dS       (u, dblk) = ((j-24)/4, (j-24)%4)
-  // P = exp2(S sl2 - lse2) is formed on the VALU during the dP steps, and
-  // dS = P (dP - delta) during the dV steps, beside the running MFMAs.
+  // P = exp2(S sl2 - lse2) is formed on the VALU during the E steps, and
+  // dS = P (dP - delta) = -(P E) during the dV steps, beside the running
+  // MFMAs: the V tile holds -V, so E ends at delta - dP (one multiply per
+  // element instead of a subtraction and a multiply).
   bf16x8 ds_keep[2];  // the last tile's packed dS (both k-steps), stored at the next step's top
   auto tile = [&](auto masked_tag, int buf, int cthr, int kmax, int qmax) {
     constexpr bool MASKED = decltype(masked_tag)::value;
-    const uint8_t* qt_ = smem[buf][0];
-    const uint8_t* ot_ = smem[buf][1];
+    const uint8_t* qt_ = &smem[0][0][0];
+    const uint8_t* ot_ = &smem[0][1][0];
     const float* lse_ = stat[buf][0];
     const float* dlt_ = stat[buf][1];
-    const int ro = opaque(roff0), vo = opaque(voff0);
-    const int to0 = opaque(toff0), to1 = opaque(toff1);
+    // The buffer offset (a multiple of 16 KB) is folded into the per-lane
+    // bases: the swizzle XORs change only bits 5-7 of an offset below 8 KB.
+    const int bo = buf * 2 * kKvTile;
+    const int ro = opaque(roff0 + bo), vo = opaque(voff0);
+    const int to0 = opaque(toff0 + bo), to1 = opaque(toff1 + bo);
     auto ld = [](const uint8_t* p) { return *reinterpret_cast<const bf16x8*>(p); };
     auto fetch = [&](int j, bf16x8& A, bf16x8& B) {
       if (j < 8) {
@@ -580,9 +599,9 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
       qlim = opaque(qmax - 4 * h);
       kbad = kc >= kmax;
     }
-    f32x16 sv, dpv;
+    f32x16 sv, dpv, dinit;
     bf16x8 A[2], B[2], pb[2], db[2];
-    f32x4 st[2];  // lse2 / delta quads, loaded two steps before use
+    f32x4 st[2];  // lse2 quads, loaded two steps before use
     fetch(0, A[0], B[0]);
     fetch(1, A[1], B[1]);
     __builtin_amdgcn_sched_barrier(0);
@@ -592,7 +611,7 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
       if (j < 8) {
         sv = mfma32x32x16(A[sl], kreg[j], j == 0 ? f32x16{} : sv);
       } else if (j < 16) {
-        dpv = mfma32x32x16(A[sl], B[sl], j == 8 ? f32x16{} : dpv);
+        dpv = mfma32x32x16(A[sl], B[sl], j == 8 ? dinit : dpv);
       } else if (j < 24) {
         const int i = j - 16;
         dv[i & 3] = mfma32x32x16(A[sl], pb[i >> 2], dv[i & 3]);
@@ -601,14 +620,18 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
         dk[i & 3] = mfma32x32x16(A[sl], db[i >> 2], dk[i & 3]);
       }
       if (j + 2 < 32) fetch(j + 2, A[sl], B[sl]);
-      // statistics: lse2 quad w at j = 7 + 2w, delta quad w at j = 16 + 2w
+      // statistics: lse2 quad w at j = 7 + 2w; delta (all four quads) at j = 5
       if (j >= 7 && j <= 13 && (j & 1)) {
         const int w = (j - 7) >> 1;
         st[w & 1] = *reinterpret_cast<const f32x4*>(&lse_[8 * w + 4 * h]);
       }
-      if (j >= 16 && j <= 22 && !(j & 1)) {
-        const int w = (j - 16) >> 1;
-        st[w & 1] = *reinterpret_cast<const f32x4*>(&dlt_[8 * w + 4 * h]);
+      if (j == 5) {  // delta of the lane's 16 queries, the dP accumulator's start
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dlt_[8 * w + 4 * h]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dinit[4 * w + r] = d4[r];
+        }
       }
       // P for elements 2k, 2k+1 at j = 9 + k
       if (j >= 9 && j <= 16) {
@@ -631,8 +654,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
         const int k = j - 18;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const int v = 2 * k + e, w = v >> 2, r = v & 3;
-          dpv[v] = sv[v] * (dpv[v] - st[w & 1][r]);
+          const int v = 2 * k + e;
+          dpv[v] = -(sv[v] * dpv[v]);
         }
       }
       // Packed bf16 B operands (slot 4p + t <- element 8u + 4(t/2) + 2(t%2) + p)

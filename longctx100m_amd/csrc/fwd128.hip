@@ -123,9 +123,20 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
       qreg[t] = *reinterpret_cast<const bf16x8*>(qbase + (int64_t)row * qs + 16 * t + 8 * hh);
   }
 
-  // K row 32mb + kc, dims 16t + 8hh: roff0 ^ (32 t) + mb * 32 rows.
+  // LDS offsets of the lane's operand fragments, computed once and kept in
+  // registers (the swizzle XORs would otherwise be redone on every tile):
+  //   K row 32mb + kc, dims 16t + 8hh: koff[t] + mb * 32 rows;
+  //   V^T, PV step i: voff0/1[i % 4] + (i / 4) * 16 rows.
   const int roff0 = t128::row_chunk_off(kc, hh);
   const int toff0 = t128::tr32_off(0, lane), toff1 = t128::tr32_off(1, lane);
+  int koff[8], voff0[4], voff1[4];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) koff[t] = opaque(roff0 ^ (32 * t));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    voff0[u] = opaque(toff0 ^ (64 * u));
+    voff1[u] = opaque(toff1 ^ (64 * u));
+  }
   const int64_t wq_first = a.q_pos0 + qw0;
 
   f32x16 o[4];
@@ -135,24 +146,23 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
   float mtrue = -INFINITY;  // exact running maximum (log2 units)
   float lsum = 0.f;         // lane-partial sum of p relative to mrun
 
-  auto kread = [](const uint8_t* kt, int ro, int i) {  // S step i: t = i / 2, mb = i % 2
-    return *reinterpret_cast<const bf16x8*>(kt + ((ro ^ (32 * (i >> 1))) + (i & 1) * 32 * t128::kRowBytes));
+  auto kread = [&](const uint8_t* kt, int i) {  // S step i: t = i / 2, mb = i % 2
+    return *reinterpret_cast<const bf16x8*>(kt + koff[i >> 1] + (i & 1) * 32 * t128::kRowBytes);
   };
-  auto vread = [](const uint8_t* vt, int to0, int to1, int i) {  // PV step i: u = i / 4, dblk = i % 4
-    const int o0 = (to0 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
-    const int o1 = (to1 ^ (64 * (i & 3))) + (i >> 2) * 16 * t128::kRowBytes;
+  auto vread = [&](const uint8_t* vt, int i) {  // PV step i: u = i / 4, dblk = i % 4
+    const int o0 = voff0[i & 3] + (i >> 2) * 16 * t128::kRowBytes;
+    const int o1 = voff1[i & 3] + (i >> 2) * 16 * t128::kRowBytes;
     return concat_bf16x4(t128::ds_read_tr(vt + o0), t128::ds_read_tr(vt + o1));
   };
 
   // S^T of tile 0 (no softmax to overlap yet).
   auto scores_only = [&](const uint8_t* kt, f32x16 (&s)[2]) {
-    const int ro = opaque(roff0);
-    bf16x8 A[2] = {kread(kt, ro, 0), kread(kt, ro, 1)};
+    bf16x8 A[2] = {kread(kt, 0), kread(kt, 1)};
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       s[i & 1] = mfma32x32x16(A[i & 1], qreg[i >> 1], i < 2 ? f32x16{} : s[i & 1]);
-      if (i + 2 < 16) A[i & 1] = kread(kt, ro, i + 2);
+      if (i + 2 < 16) A[i & 1] = kread(kt, i + 2);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -165,8 +175,6 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
                        f32x16 (&sc)[2], f32x16 (&sn)[2], int cthr, int kmax) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool HAS_NEXT = decltype(next_tag)::value;
-    const int ro = opaque(roff0);
-    const int to0 = opaque(toff0), to1 = opaque(toff1);
     int kq = 0, klim = 0;
     if constexpr (MASKED) {
       kq = opaque(4 * hh - kc);
@@ -174,8 +182,8 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
     }
     bf16x8 A[2], B[2], pb[4];
     if constexpr (HAS_NEXT) {
-      A[0] = kread(kt, ro, 0);
-      A[1] = kread(kt, ro, 1);
+      A[0] = kread(kt, 0);
+      A[1] = kread(kt, 1);
     }
     float pmax = -INFINITY, muse = 0.f;
     __builtin_amdgcn_sched_barrier(0);
@@ -183,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
     for (int i = 0; i < 16; ++i) {
       if constexpr (HAS_NEXT) {
         sn[i & 1] = mfma32x32x16(A[i & 1], qreg[i >> 1], i < 2 ? f32x16{} : sn[i & 1]);
-        if (i + 2 < 16) A[i & 1] = kread(kt, ro, i + 2);
+        if (i + 2 < 16) A[i & 1] = kread(kt, i + 2);
       }
       if (i < 4) {  // mask and maximum, 8 scores per step
 #pragma unroll
@@ -232,14 +240,14 @@ __global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
               f32x4{sc[mb][e0 + 1], sc[mb][e0 + 3], sc[mb][e0 + 5], sc[mb][e0 + 7]});
         }
       }
-      if (i == 14) B[0] = vread(vt, to0, to1, 0);
-      if (i == 15) B[1] = vread(vt, to0, to1, 1);
+      if (i == 14) B[0] = vread(vt, 0);
+      if (i == 15) B[1] = vread(vt, 1);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       o[i & 3] = mfma32x32x16(B[i & 1], pb[i >> 2], o[i & 3]);
-      if (i + 2 < 16) B[i & 1] = vread(vt, to0, to1, i + 2);
+      if (i + 2 < 16) B[i & 1] = vread(vt, i + 2);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
