@@ -7,9 +7,13 @@
 // normalised output o = acc / l and statistics (m, l); lc_attn_merge folds
 // them into the ring's running state.
 //
-// Work split: workgroup = 4 waves x 32 queries of one (batch, query head).
-// Q^T lives in VGPRs as the MFMA B operand; 64-key tiles of K and V live in
-// LDS as swizzled row-major tiles (tile128.h), filled by LDS DMA.
+// Work split: workgroup = 8 waves x 32 queries of one (batch, query head),
+// one workgroup per CU (two waves per SIMD).  Q^T lives in VGPRs as the MFMA
+// B operand; 64-key tiles of K and V live in LDS as swizzled row-major tiles
+// (tile128.h), filled by LDS DMA.  Moving a tile into LDS costs SIMD cycles
+// in proportion to its bytes, so the tiles are shared by as many queries as
+// two waves per SIMD allow (256: half the DMA per MFMA of a 128-query
+// workgroup).
 //   S^T = K Q^T     A = K rows (ds_read_b128), B = Q^T
 //   O^T += V^T P^T  A = V^T (transposed reads of the V tile),
 //                   B = P^T straight from the S^T accumulators
@@ -44,7 +48,7 @@ namespace lc {
 namespace {
 
 constexpr int D = 128;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kQW = 32;             // queries per wave
 constexpr int BM = kWaves * kQW;    // queries per workgroup
 constexpr int BN = 64;              // keys per tile
@@ -66,7 +70,7 @@ struct Fwd128Args {
   float sl2;       // scale * log2(e)
 };
 
-__global__ __launch_bounds__(256, 2) void fwd128_kernel(Fwd128Args a) {
+__global__ __launch_bounds__(512, 1) void fwd128_kernel(Fwd128Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
 
@@ -349,7 +353,7 @@ hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const v
   a.causal = p.causal ? 1 : 0;
   a.accumulate = accumulate ? 1 : 0;
   a.sl2 = p.scale * kLog2e;
-  hipLaunchKernelGGL(fwd128_kernel, dim3(a.n_qtiles * p.Hq * p.B), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(fwd128_kernel, dim3(a.n_qtiles * p.Hq * p.B), dim3(64 * kWaves), 0, s, a);
   return hipGetLastError();
 }
 
