@@ -7,13 +7,15 @@
 // normalised output o = acc / l and statistics (m, l); lc_attn_merge folds
 // them into the ring's running state.
 //
-// Work split: workgroup = 8 waves x 32 queries of one (batch, query head),
-// one workgroup per CU (two waves per SIMD).  Q^T lives in VGPRs as the MFMA
-// B operand; 64-key tiles of K and V live in LDS as swizzled row-major tiles
-// (tile128.h), filled by LDS DMA.  Moving a tile into LDS costs SIMD cycles
-// in proportion to its bytes, so the tiles are shared by as many queries as
-// two waves per SIMD allow (256: half the DMA per MFMA of a 128-query
-// workgroup).
+// Work split: workgroup = NW waves x 32 queries of one (batch, query head),
+// two waves per SIMD.  Q^T lives in VGPRs as the MFMA B operand; 64-key
+// tiles of K and V live in LDS as swizzled row-major tiles (tile128.h),
+// filled by LDS DMA.  Moving a tile into LDS costs SIMD cycles in proportion
+// to its bytes, so a hop whose keys all precede its queries (no causal
+// diagonal) runs NW = 8 (256 queries share each tile, one workgroup per CU:
+// half the DMA per MFMA); a hop that straddles the diagonal runs NW = 4 (two
+// workgroups per CU), whose shorter query range wastes less of each
+// workgroup's tile walk on waves that have no key left to see.
 //   S^T = K Q^T     A = K rows (ds_read_b128), B = Q^T
 //   O^T += V^T P^T  A = V^T (transposed reads of the V tile),
 //                   B = P^T straight from the S^T accumulators
@@ -48,9 +50,7 @@ namespace lc {
 namespace {
 
 constexpr int D = 128;
-constexpr int kWaves = 8;
 constexpr int kQW = 32;             // queries per wave
-constexpr int BM = kWaves * kQW;    // queries per workgroup
 constexpr int BN = 64;              // keys per tile
 constexpr int kTileBytes = BN * t128::kRowBytes;
 constexpr float kRescaleSlack = 8.0f;  // log2 units
@@ -70,7 +70,10 @@ struct Fwd128Args {
   float sl2;       // scale * log2(e)
 };
 
-__global__ __launch_bounds__(512, 1) void fwd128_kernel(Fwd128Args a) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void fwd128_kernel(Fwd128Args a) {
+  constexpr int kWaves = NW;
+  constexpr int BM = kWaves * kQW;  // queries per workgroup
   __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
 
@@ -345,7 +348,10 @@ hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const v
   a.Hq = p.Hq;
   a.Hkv = p.Hkv;
   a.group = p.Hq / p.Hkv;
-  a.n_qtiles = (p.Nq + BM - 1) / BM;
+  // No causal diagonal in this launch: every key precedes every query.
+  const bool full = !p.causal || p.k_pos0 + p.Nk - 1 <= p.q_pos0;
+  const int bm = (full ? 8 : 4) * kQW;
+  a.n_qtiles = (p.Nq + bm - 1) / bm;
   a.q_pos0 = p.q_pos0;
   a.k_pos0 = p.k_pos0;
   a.valid = p.valid;
@@ -353,7 +359,10 @@ hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const v
   a.causal = p.causal ? 1 : 0;
   a.accumulate = accumulate ? 1 : 0;
   a.sl2 = p.scale * kLog2e;
-  hipLaunchKernelGGL(fwd128_kernel, dim3(a.n_qtiles * p.Hq * p.B), dim3(64 * kWaves), 0, s, a);
+  if (full)
+    hipLaunchKernelGGL(fwd128_kernel<8>, dim3(a.n_qtiles * p.Hq * p.B), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL(fwd128_kernel<4>, dim3(a.n_qtiles * p.Hq * p.B), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
