@@ -55,6 +55,9 @@ FWD_CASES = [
     (128, 192, 2, 2, 128, 0, 0, False, None),     # non-causal
     (96, 64, 3, 1, 128, 0, 64, True, None),       # partly fully-masked rows
     (64, 64, 1, 1, 128, 0, 64, True, None),       # keys after every query
+    # full hops (every key before every query) run the 256-query workgroups
+    (520, 300, 2, 2, 128, 1000, 0, True, 250),    # valid_length inside the shard, 3 tiles
+    (257, 129, 8, 2, 128, 0, 0, False, 100),      # GQA 4, non-causal, one-row tail tile
 ]
 
 
