@@ -11,8 +11,10 @@
 // the S partials by log-sum-exp.
 //
 // Per wave: Q^T of the R rows in VGPRs (B operand, rows >= R are zero);
-// 32-key tiles of K and V double-buffered in LDS by direct global->LDS loads
-// (tile128.h layout); S^T = K Q^T, exact online softmax per row in the log2
+// 32-key tiles: K straight into VGPRs (the A operand of S^T = K Q^T wants each
+// lane's 8 dims of one key, which a 16-byte global load gives), V
+// double-buffered in LDS by direct global->LDS loads (tile128.h layout), both
+// one tile ahead; S^T = K Q^T, exact online softmax per row in the log2
 // domain, O^T += V^T P^T with V^T from transposed LDS reads.
 #include "common.h"
 #include "kernels.h"
@@ -36,14 +38,12 @@ namespace {
 
 constexpr int D = 128;
 constexpr int TK = 32;  // keys per tile
-// K/V tiles in LDS per workgroup: the one in use and kStages - 1 in flight.
-// LDS bounds stages x workgroups per CU; measured one C4 layer (262,144 keys,
-// 8 KV heads): 2 stages (5 workgroups per CU) 4.76 TB/s, 3 stages (3 per CU)
-// 5.24 TB/s, 4 and 5 stages (2 per CU) 4.72 and 4.79 TB/s: a lone wave per
-// SIMD cannot hide its own MFMA and LDS latencies.
-constexpr int kStages = 3;
-constexpr int kLdInst = 2 * TK / 4;  // DMA instructions per K+V tile (4 rows each)
-static_assert((kStages - 2) * kLdInst < 64, "vmcnt immediate");
+// V tiles in LDS per workgroup: the one in use and one in flight.  With K
+// staged in LDS as well, one C4 layer (262,144 keys, 8 KV heads) read the
+// cache at 4.72-5.24 TB/s (2-5 stages); K in VGPRs (the LDS round trip costs
+// SIMD cycles per byte) and eight one-wave workgroups per CU (the register
+// limit of two waves per SIMD) read it at 5.68 TB/s.
+constexpr int kStages = 2;
 constexpr int KS = D / 32;
 constexpr int DB = D / 16;
 constexpr int kTileBytes = TK * t128::kRowBytes;
@@ -62,20 +62,7 @@ struct DecodeArgs {
   float sl2;  // scale * log2(e)
 };
 
-// Waits until at most n tiles' loads are outstanding (n < kStages - 1).
-__device__ __forceinline__ void wait_tiles(int n) {
-  static_assert(kStages <= 6, "wait_tiles cases");
-  switch (n) {
-    case 0: t128::wait_vmem(); break;
-    case 1: t128::wait_vmem_but<kLdInst>(); break;
-    case 2: t128::wait_vmem_but<(2 * kLdInst < 64 ? 2 * kLdInst : 0)>(); break;
-    case 3: t128::wait_vmem_but<(3 * kLdInst < 64 ? 3 * kLdInst : 0)>(); break;
-    default: t128::wait_vmem_but<(4 * kLdInst < 64 ? 4 * kLdInst : 0)>(); break;
-  }
-}
-
 __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t kbuf[kStages][kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t vbuf[kStages][kTileBytes];
 
   const int lane = threadIdx.x;
@@ -100,10 +87,21 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
 
   t128::RowLoader<TK, 1> ld;
   ld.init(ks, 0, lane);
-  auto issue = [&](int j) {  // tile j into stage j % kStages
+  auto issue = [&](int j) {  // V tile j into stage j % kStages
     const int st = j % kStages;
-    ld.load(kbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk, t128::lds_addr(kbuf) + st * kTileBytes, 0, lane);
     ld.load(vbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk, t128::lds_addr(vbuf) + st * kTileBytes, 0, lane);
+  };
+  // K tile j straight into VGPRs (no LDS round trip): lane (c, g) holds key
+  // 16 mb + c of the tile, dims 32 kk + 8 g, the A operand of S^T = K Q^T.
+  auto kload = [&](int j, bf16x8 (&kr)[2][4]) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      int64_t row = kb0 + (int64_t)j * TK + 16 * mb + c;
+      row = row < a.Nk ? row : a.Nk - 1;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        kr[mb][kk] = *reinterpret_cast<const bf16x8*>(kbase + row * ks + 32 * kk + 8 * g);
+    }
   };
 
   // Row c of this (batch, KV head): query head hk*group + c / Nq, query c % Nq.
@@ -124,13 +122,12 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   // Q is in VGPRs from here on (the compiler, which cannot count the tile
   // loads below, would otherwise wait for every load before each use of Q).
   t128::wait_vmem();
-#pragma unroll
-  for (int j = 0; j < kStages - 1; ++j)
-    if (j < ntiles) issue(j);
+  bf16x8 kra[2][KS], krb[2][KS];
+  if (ntiles > 0) {
+    issue(0);
+    kload(0, kra);
+  }
 
-  int koff[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) koff[kk] = t128::row_chunk_off(c, 4 * kk + g);
   int voff[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) voff[db] = t128::tr_off(0, 16 * db, lane);
@@ -141,13 +138,15 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   float mrow = -INFINITY;  // running max of this lane's row (log2 units)
   float lsum = 0.f;        // lane-partial sum of p
 
-  for (int j = 0; j < ntiles; ++j) {
-    // tiles j + 1 .. j + kStages - 2 (those that exist) may stay in flight
-    wait_tiles(min(kStages - 2, ntiles - 1 - j));
-    // stage (j - 1) % kStages was read by the previous iteration, whose LDS
-    // reads completed before its MFMAs consumed them
-    if (j + kStages - 1 < ntiles) issue(j + kStages - 1);
-    const uint8_t* kt = kbuf[j % kStages];
+  // Tile j: wait for V(j) in LDS and K(j) in VGPRs (both issued at tile j - 1),
+  // issue V(j + 1) into the other stage (read by tile j - 1, done) and
+  // K(j + 1) into the other register set, then compute tile j.
+  auto tile = [&](int j, bf16x8 (&kc)[2][KS], bf16x8 (&kn)[2][KS]) {
+    t128::wait_vmem();
+    if (j + 1 < ntiles) {
+      issue(j + 1);
+      kload(j + 1, kn);
+    }
     const uint8_t* vt = vbuf[j % kStages];
     const int64_t key0 = kb0 + (int64_t)j * TK;
 
@@ -156,10 +155,7 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kt + koff[kk] + mb * 16 * t128::kRowBytes);
-        sc[mb] = mfma16x16x32(ka, qreg[kk], sc[mb]);
-      }
+      for (int mb = 0; mb < 2; ++mb) sc[mb] = mfma16x16x32(kc[mb][kk], qreg[kk], sc[mb]);
     }
     // Mask: past the split / cache end, valid_length, causal (per row).
     const int64_t kmax = kb1 - key0;  // keys of this tile inside the split
@@ -198,6 +194,10 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
       const bf16x8 va = concat_bf16x4(t128::ds_read_tr(p), t128::ds_read_tr(p + 16 * t128::kRowBytes));
       o[db] = mfma16x16x32(va, pb, o[db]);
     }
+  };
+  for (int j = 0; j < ntiles; j += 2) {
+    tile(j, kra, krb);
+    if (j + 1 < ntiles) tile(j + 1, krb, kra);
   }
 
   // Partial of this split: normalised o, m (natural log), l.
@@ -290,7 +290,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S,
 // Splits per (batch, KV head): as many one-wave workgroups as fit the CUs'
 // LDS (kStages tiles each), at least two tiles per split.
 int decode_splits(const Problem& p) {
-  constexpr int kPerCu = (160 * 1024) / (kStages * 2 * kTileBytes);
+  constexpr int kLdsPerCu = (160 * 1024) / (kStages * kTileBytes);
+  constexpr int kPerCu = kLdsPerCu < 8 ? kLdsPerCu : 8;  // two waves per SIMD (registers)
   const int64_t tiles = ((int64_t)p.Nk + TK - 1) / TK;
   const int64_t want = (kPerCu * 256 + (int64_t)p.B * p.Hkv - 1) / ((int64_t)p.B * p.Hkv);
   int64_t s = want < 1 ? 1 : want;
