@@ -35,6 +35,7 @@ import threading
 import time
 
 PEAK_BF16_TFLOPS = 2516.6
+PEAK_SCLK_MHZ = 2400.0  # the shader clock the published peak assumes
 METRIC = "causal attn fwd+bwd TFLOP/s @32k bf16 shard, % MFMA peak; vs CPU ref"
 
 
@@ -184,8 +185,8 @@ class ClockSampler:
         if not self.samples:
             return None
         xs = self.samples
-        return {"mean": round(sum(xs) / len(xs), 1), "min": min(xs), "max": max(xs),
-                "samples": len(xs)}
+        return {"mean": round(sum(xs) / len(xs), 1), "median": sorted(xs)[len(xs) // 2],
+                "min": min(xs), "max": max(xs), "samples": len(xs)}
 
 
 def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
@@ -690,10 +691,17 @@ def main() -> int:
         achieved = tflops
         rl_kernel = "whole step"
         rl_units = f"{total_flops / 1e12:.3f} TFLOP per step"
+    sclk = clock.summary()
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": measured_traffic(rl_kernel, n, h, d), "kernel": rl_kernel,
-                "algorithmic": rl_units, "sclk_mhz": clock.summary(),
+                "algorithmic": rl_units, "sclk_mhz": sclk,
+                # the same fraction against the peak scaled to the mean sampled shader clock
+                # (the 2516.6 TFLOP/s peak assumes 2.4 GHz; the samples are the firmware's
+                # clock levels, so this is approximate): comparable across boxes
+                "frac_at_sampled_clock": (
+                    round(achieved / (PEAK_BF16_TFLOPS * sclk["mean"] / PEAK_SCLK_MHZ), 4)
+                    if sclk and sclk["mean"] > 0 else None),
                 "box": socket.gethostname()}
 
     cpu = None
