@@ -200,7 +200,8 @@ int bwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
 // workspace given): the dK/dV kernel stores the dS it forms and the dQ
 // kernel reads it back, so dQ costs one GEMM instead of three (S, dP and dQ).
 // The workspace holds the dS of one chunk of query rows at a time; chunks are
-// multiples of 256 rows (one dQ workgroup) of at most kStreamChunk rows.
+// multiples of 256 rows (half a dQ workgroup of 512; a workgroup past the
+// chunk's end leaves its waves idle) of at most kStreamChunk rows.
 // Returns the chunk's row count, 0 when the shape or workspace does not allow
 // it.
 int64_t ds_chunk_rows(const lc::Problem& p, size_t ws_bytes) {

@@ -287,10 +287,12 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 
 // dQ^T += K^T dS^T with dS read back from the exchange blocks dkdv128 wrote
 // for the same (query shard, KV shard) pair: no score recomputation, one
-// GEMM.  Workgroup = 8 waves x 32 queries of one (batch, query head); 64-key
+// GEMM.  Workgroup = 16 waves x 32 queries of one (batch, query head); 64-key
 // tiles of K (shared, LDS DMA) and each wave's two dS blocks of the tile
-// (its own, LDS DMA), one barrier per tile.  Eight waves share each K tile:
-// 5.9 ms per 32k x 32k x 16-head hop against 6.4 ms with four.
+// (its own, LDS DMA), one barrier per tile.  The more waves share each K tile,
+// the fewer bytes cross into LDS per MFMA: per 32k x 32k x 16-head hop four
+// waves took 6.4 ms, eight 5.9 ms, sixteen (dS one tile ahead instead of two)
+// ~0.25 ms less again.
 //   A = K^T (transposed reads of the K tile, tr32_off), B = dS^T (transposed
 //   reads of the dS blocks, same key order)
 // Column j of the accumulator is query qw0 + ds_query(j): the transposed read
@@ -300,8 +302,8 @@ __global__ __launch_bounds__(256, 2) void dq128_kernel(Bwd128Args a) {
 // every query of the wave) is replaced by zeros; inside a written block every
 // masked score already has dS = 0.
 constexpr int kDsWaveBytes = 2 * 2 * kDsBlockElems;  // a wave's two blocks of one tile
-constexpr int kDsStages = 3;  // dS tiles in LDS: the one in use and two in flight
-constexpr int kDsNW = 8;      // waves per workgroup
+constexpr int kDsStages = 2;  // dS tiles in LDS: the one in use and one in flight
+constexpr int kDsNW = 16;     // waves per workgroup (4 per SIMD: <= 128 VGPRs)
 constexpr int kDsBM = kDsNW * kDqQW;  // queries per workgroup
 
 __device__ __forceinline__ int ds_query(int j) {
@@ -309,8 +311,8 @@ __device__ __forceinline__ int ds_query(int j) {
   return 16 * (c >> 3) + 4 * cb + ((c >> 2) & 1) + 2 * (c & 1) + 8 * ((c >> 1) & 1);
 }
 
-// LDS: K double-buffered (one tile ahead), dS in kDsStages buffers (two tiles
-// ahead, the kernel streams them from HBM): 128 KB, one workgroup per CU.
+// LDS: K double-buffered and dS in kDsStages buffers, both one tile ahead (the
+// dS stream comes from HBM): 160 KB, one workgroup per CU.
 __global__ __launch_bounds__(64 * kDsNW, 1) void dqds128_kernel(Bwd128Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kDqTile];
   __shared__ __attribute__((aligned(1024))) uint8_t dsbuf[kDsStages][kDsNW][kDsWaveBytes];
@@ -356,11 +358,11 @@ __global__ __launch_bounds__(64 * kDsNW, 1) void dqds128_kernel(Bwd128Args a) {
   const uint32_t ds_lds = t128::lds_addr(dsbuf) + wave * kDsWaveBytes;
   t128::RowLoader<kDqBN, kDsNW> ld;
   ld.init(ks, wave, lane);
-  // dS of tile j (blocks 2j, 2j+1) as exactly four DMA instructions, so the
-  // wait for the older loads is a fixed vmcnt(4); a missing block 2j+1 (past
-  // the keys) re-reads block 2j, and its operand is zeroed below.
+  // dS of tile j (blocks 2j, 2j+1) as four DMA instructions (none for a tile
+  // the wave does not compute); a missing block 2j+1 (past the keys) re-reads
+  // block 2j, and its operand is zeroed below.
   auto load_ds = [&](int j) {
-    if (j >= nt_w) return false;
+    if (j >= nt_w) return;
     const int nb = min(2, nkb - 2 * j);
     const uint16_t* src = dsrow + (int64_t)(2 * j) * kDsBlockElems;
     const uint32_t dst = ds_lds + (j % kDsStages) * kDsNW * kDsWaveBytes;
@@ -369,11 +371,9 @@ __global__ __launch_bounds__(64 * kDsNW, 1) void dqds128_kernel(Bwd128Args a) {
       const int si = i < 2 * nb ? i : i - 2;
       t128::dma_b128_nt(src + si * (kDsBlockElems / 2), 16u * lane, dst + i * 1024);
     }
-    return true;
   };
   ld.load(kbase, ks, 0, a.Nk, kbuf_lds, wave, lane);
   load_ds(0);
-  bool ahead = load_ds(1);  // the last loads issued are a dS tile not needed yet
 
   // B operand read of k-step 0, k-half 0: lane (group G, index i) addresses
   // row key(hh, 0, t) of half G % 2, chunk g = i % 4 (u = g / 2, byte 8 (g % 2)).
@@ -390,14 +390,11 @@ __global__ __launch_bounds__(64 * kDsNW, 1) void dqds128_kernel(Bwd128Args a) {
   for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
 
   for (int j = 0; j < ntiles; ++j) {
-    if (ahead)
-      t128::wait_vmem_but<4>();  // K_j and dS_j, not dS_{j+1}
-    else
-      t128::wait_vmem();
+    t128::wait_vmem();  // K_j and dS_j
     __syncthreads();
     if (j + 1 < ntiles)
       ld.load(kbase, ks, (j + 1) * kDqBN, a.Nk, kbuf_lds + ((j + 1) & 1) * kDqTile, wave, lane);
-    ahead = load_ds(j + 2);
+    load_ds(j + 1);
     if (j >= nt_w) continue;
     const uint8_t* kt = kbuf[j & 1];
     const uint8_t* dt = dsbuf[j % kDsStages][wave];
