@@ -667,3 +667,46 @@ def test_full_size_c2_c3_spot_check(ra, gpu):
     assert max(kerr) / max(kref) <= 2e-2
     assert max(verr) / max(vref) <= 2e-2
     assert torch.isfinite(out.float()).all() and torch.isfinite(dq.float()).all()
+
+
+def _random_cases(seed, n):
+    """Random d=128 bf16 shapes, GQA groups, positions and masks (drawn once)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        hkv = int(rng.choice([1, 2]))
+        out.append(dict(b=int(rng.integers(1, 3)), nq=int(rng.integers(1, 700)),
+                        nk=int(rng.integers(1, 700)), hkv=hkv, hq=hkv * int(rng.choice([1, 2, 4])),
+                        causal=bool(rng.integers(0, 2)), q_pos0=int(rng.integers(0, 1500)),
+                        k_pos0=int(rng.integers(0, 1500)),
+                        valid_length=None if rng.integers(0, 3) else int(rng.integers(1, 2500))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(2026, 24), ids=lambda c: "q{nq}k{nk}h{hq}/{hkv}".format(**c))
+def test_random_shapes_fwd_and_shared_ds_bwd(ra, gpu, case):
+    """Random shapes through the benched kernels (forward, preprocess, dS-sharing backward) against
+    the fp64 dense oracle at the bf16 bar: query and key counts that are not multiples of any tile,
+    offsets that make hops full, diagonal, partial or empty, valid_length cuts, GQA 1/2/4."""
+    c = dict(case)
+    b, nq, nk, hq, hkv = c.pop("b"), c.pop("nq"), c.pop("nk"), c.pop("hq"), c.pop("hkv")
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    q = _t(gpu, rng.standard_normal((b, nq, hq, 128)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((b, nk, hkv, 128)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((b, nk, hkv, 128)), gpu.bfloat16)
+    do = _t(gpu, rng.standard_normal((b, nq, hq, 128)), gpu.bfloat16)
+    o32, m, l = ra.fwd_shard(q, k, v, **c)
+    out = o32.to(gpu.bfloat16)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    ws = gpu.empty(max(256, ra.bwd_shard_workspace_bytes(q, k)), dtype=gpu.uint8, device="cuda")
+    dq = gpu.zeros((b, nq, hq, 128), dtype=gpu.float32, device="cuda")
+    dk = gpu.zeros((b, nk, hkv, 128), dtype=gpu.float32, device="cuda")
+    dv = gpu.zeros_like(dk)
+    ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, workspace=ws, **c)
+    gpu.cuda.synchronize()
+    eo, em, el = dense.attention_fwd(_np(q), _np(k), _np(v), **c)
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **c)
+    assert norm_rel(_np(o32), eo) <= BF16_TOL
+    assert norm_rel(_np(dq), edq) <= BF16_TOL
+    assert norm_rel(_np(dk), edk) <= BF16_TOL
+    assert norm_rel(_np(dv), edv) <= BF16_TOL
