@@ -4,8 +4,9 @@ recompute backward, on one MI355X (BASELINE configs 2 and 3).
 
 Workload (one "step"): rank 7 of an 8-rank ring, a 32768-token bf16 local
 query shard, Hq = Hkv = 16, d = 128.  Forward: the diagonal KV shard plus 7
-preceding full KV shards, each hop's partial merged by log-sum-exp into the
-running state (fwd kernel + merge kernel per hop).  Backward: preprocess
+preceding full KV shards, each hop's result merged by log-sum-exp into the
+running state in the forward kernel's epilogue, then a cast to the bf16
+output.  Backward: preprocess
 (delta, LSE), then per hop the dK/dV kernel (per-shard dK/dV, as they would
 travel back around the ring), which also stores dS (bf16) in a workspace,
 and the dQ kernel that reads it back (accumulating dQ across shards);

@@ -49,6 +49,7 @@ enum lc_status {
 
 /* Flags for lc_attn_shape_t.flags. */
 #define LC_FLAG_PRECISE 1u /* bf16 inputs: use the fp32-math kernels instead of bf16 MFMA */
+#define LC_FLAG_ACCUMULATE 2u /* lc_attn_fwd_shard: merge into the running (o, m, l) */
 
 /* One (query shard x KV shard) problem. */
 typedef struct lc_attn_shape {
@@ -78,7 +79,15 @@ typedef struct lc_attn_mask {
 /* One ring hop's forward: attention of the query shard over one KV shard
  * (online softmax over the shard, rs:57-106 / rs:15-55).  Writes the shard's
  * normalised partial output o [B, q_tokens, heads_q, D] fp32 and its
- * statistics m, l [B, heads_q, q_tokens] fp32. */
+ * statistics m, l [B, heads_q, q_tokens] fp32.
+ * With LC_FLAG_ACCUMULATE in shape->flags, o, m and l hold a running state
+ * (an earlier hop's result, or lc_attn_init_state's) and the hop's result is
+ * merged into it in place with lc_attn_merge's weights: the reference's
+ * (m, l, acc) state carried from hop to hop (rs:195-225), with no partial
+ * buffers and no merge pass.  A pair with no unmasked key leaves the state
+ * as it is.  lc_attn_decode, lc_attn_decode_static and the ring descriptor
+ * reject the flag (LC_ERR_INVALID); the backward, merge, init and cast entry
+ * points ignore it. */
 int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
                       const void* k, const void* v, float* o, float* m, float* l, void* stream);
 

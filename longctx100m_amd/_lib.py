@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "liblongctx100m_attn.so"
 LC_DTYPE_F32 = 0
 LC_DTYPE_BF16 = 1
 LC_FLAG_PRECISE = 1
+LC_FLAG_ACCUMULATE = 2
 
 LC_OK = 0
 LC_ERR_INVALID = 1

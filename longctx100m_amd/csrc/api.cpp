@@ -84,6 +84,7 @@ lc::Problem make_problem(const lc_attn_shape_t* s, const lc_attn_mask_t* m) {
   p.D = s->head_dim;
   p.dtype = s->dtype;
   p.precise = (s->flags & LC_FLAG_PRECISE) != 0;
+  p.accumulate = false;  // read by lc_attn_fwd_shard alone
   p.q_pos0 = m ? m->q_pos0 : 0;
   p.k_pos0 = m ? m->k_pos0 : 0;
   p.valid = (m && m->valid_length >= 0) ? m->valid_length : std::numeric_limits<int64_t>::max();
@@ -120,7 +121,7 @@ int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
   hipError_t e = hipSuccess;
   if (use_mfma(p, q, k, v, nullptr) && p.D == 128) {
     if (p.Nk <= kStreamChunk) {
-      e = lc::launch_fwd128(p, q, k, v, o, m, l, st);
+      e = lc::launch_fwd128(p, q, k, v, o, m, l, st, -1, p.accumulate);
     } else {
       const size_t row_bytes = (size_t)p.Hkv * p.D * 2;  // bf16 K/V row
       bool first = true;
@@ -131,7 +132,7 @@ int fwd_shard(const lc::Problem& p, const void* q, const void* k, const void* v,
         if (!pair_active(pc)) continue;  // the running state is unchanged
         const char* kc = static_cast<const char*>(k) + c0 * row_bytes;
         const char* vc = static_cast<const char*>(v) + c0 * row_bytes;
-        e = lc::launch_fwd128(pc, q, kc, vc, o, m, l, st, p.Nk, !first);
+        e = lc::launch_fwd128(pc, q, kc, vc, o, m, l, st, p.Nk, p.accumulate || !first);
         first = false;
       }
     }
@@ -280,6 +281,8 @@ int check_ring(const lc_ring_desc_t* d) {
     return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", d->dtype);
   if (d->head_dim > 256)
     return set_error(LC_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", d->head_dim);
+  if (d->flags & LC_FLAG_ACCUMULATE)
+    return set_error(LC_ERR_INVALID, "LC_FLAG_ACCUMULATE applies to lc_attn_fwd_shard only");
   return LC_OK;
 }
 
@@ -290,19 +293,12 @@ lc::Problem ring_problem(const lc_ring_desc_t* d, int64_t q_pos0, int64_t k_pos0
   return make_problem(&s, &m);
 }
 
-struct FwdWs {
-  float* o_run;
-  float* o_part;
-  float* m_part;
-  float* l_part;
-};
-
 size_t round_up(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The running fp32 output; m and l are carried in the caller's outputs.
 size_t fwd_ws_bytes(const lc_ring_desc_t* d) {
   const size_t n_o = (size_t)d->batch * d->local_tokens * d->heads_q * d->head_dim;
-  const size_t n_s = (size_t)d->batch * d->heads_q * d->local_tokens;
-  return 2 * round_up(n_o * 4) + 2 * round_up(n_s * 4);
+  return round_up(n_o * 4);
 }
 
 size_t bwd_ws_bytes(const lc_ring_desc_t* d) {
@@ -345,10 +341,12 @@ int lc_attn_fwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
   if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
   if (mask && mask->valid_length < -1)
     return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
-  const lc::Problem p = make_problem(shape, mask);
+  lc::Problem p = make_problem(shape, mask);
+  p.accumulate = (shape->flags & LC_FLAG_ACCUMULATE) != 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (p.Nq == 0) return LC_OK;
-  if (!pair_active(p)) {
+  if (!pair_active(p)) {  // accumulate: alpha = 1, p = 0 leave the running state as it is
+    if (p.accumulate) return LC_OK;
     hipError_t e = lc::launch_init_state(p.B, p.Nq, p.Hq, p.D, o, m, l, st);
     return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_fwd_shard init");
   }
@@ -366,6 +364,8 @@ int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, con
                    size_t workspace_bytes, void* stream) {
   if (int rc = check_shape(shape)) return rc;
   if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (shape->flags & LC_FLAG_ACCUMULATE)
+    return set_error(LC_ERR_INVALID, "LC_FLAG_ACCUMULATE applies to lc_attn_fwd_shard only");
   if (mask && mask->valid_length < -1)
     return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
   const lc::Problem p = make_problem(shape, mask);
@@ -393,6 +393,8 @@ int lc_attn_decode_static(const lc_attn_shape_t* shape, const lc_attn_mask_t* ma
                           void* stream) {
   if (int rc = check_shape(shape)) return rc;
   if (!q || !k || !v || !o || !m || !l) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (shape->flags & LC_FLAG_ACCUMULATE)
+    return set_error(LC_ERR_INVALID, "LC_FLAG_ACCUMULATE applies to lc_attn_fwd_shard only");
   if (mask && mask->valid_length < -1)
     return set_error(LC_ERR_INVALID, "valid_length must be -1 (None) or non-negative");
   const lc::Problem p = make_problem(shape, mask);
@@ -538,12 +540,7 @@ int lc_ring_fwd_with_stats(const lc_ring_desc_t* d, const void* const* qs, const
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int n = d->local_tokens;
   const size_t n_o = (size_t)d->batch * n * d->heads_q * d->head_dim;
-  const size_t n_s = (size_t)d->batch * d->heads_q * n;
-  char* w = static_cast<char*>(workspace);
-  float* o_run = reinterpret_cast<float*>(w);
-  float* o_part = reinterpret_cast<float*>(w + round_up(n_o * 4));
-  float* m_part = reinterpret_cast<float*>(w + 2 * round_up(n_o * 4));
-  float* l_part = reinterpret_cast<float*>(w + 2 * round_up(n_o * 4) + round_up(n_s * 4));
+  float* o_run = static_cast<float*>(workspace);
   const int64_t q_pos0 = d->q_position_start >= 0 ? d->q_position_start : (int64_t)d->rank * n;
 
   // Hops with at least one unmasked pair; the others leave the reference's
@@ -559,22 +556,16 @@ int lc_ring_fwd_with_stats(const lc_ring_desc_t* d, const void* const* qs, const
     LC_TRY_HIP(lc::launch_cast(o_run, out, (int64_t)n_o, d->dtype, st), "lc_ring_fwd_with_stats cast");
     return LC_OK;
   }
+  // The first hop writes (o_run, m, l); every later hop LSE-merges its result
+  // into them in the forward's epilogue (the weights of lc_attn_merge), the
+  // reference's (m, l, acc) state carried from hop to hop (rs:195-225).
   for (size_t i = 0; i < owners.size(); ++i) {
     const int owner = owners[i];
-    const lc::Problem p = ring_problem(d, q_pos0, (int64_t)owner * n);
-    if (i == 0) {
-      if (int rc = fwd_shard(p, qs[d->rank], ks[owner], vs[owner], o_run, m, l, st)) return rc;
-    } else {
-      if (int rc = fwd_shard(p, qs[d->rank], ks[owner], vs[owner], o_part, m_part, l_part, st))
-        return rc;
-      const bool last = (i + 1 == owners.size());
-      LC_TRY_HIP(lc::launch_merge(d->batch, n, d->heads_q, d->head_dim, o_run, m, l, o_part,
-                                  m_part, l_part, last ? out : nullptr, d->dtype, st),
-                 "lc_ring_fwd_with_stats merge");
-    }
+    lc::Problem p = ring_problem(d, q_pos0, (int64_t)owner * n);
+    p.accumulate = i > 0;
+    if (int rc = fwd_shard(p, qs[d->rank], ks[owner], vs[owner], o_run, m, l, st)) return rc;
   }
-  if (owners.size() == 1)
-    LC_TRY_HIP(lc::launch_cast(o_run, out, (int64_t)n_o, d->dtype, st), "lc_ring_fwd_with_stats cast");
+  LC_TRY_HIP(lc::launch_cast(o_run, out, (int64_t)n_o, d->dtype, st), "lc_ring_fwd_with_stats cast");
   return LC_OK;
 }
 

@@ -50,7 +50,8 @@ struct FwdArgs {
   int Nq, Nk, Hq, Hkv, group, n_qtiles;
   int64_t q_pos0, k_pos0, valid;
   int causal;
-  float sl2;  // scale * log2(e)
+  int accumulate;  // merge into the running (o, m, l) instead of writing them
+  float sl2;       // scale * log2(e)
 };
 
 template <int D>
@@ -209,20 +210,32 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(FwdArgs a) {
   }
 
   // Epilogue: o = acc / l, m in natural-log units, l as the reference defines it.
+  // accumulate: LSE-merge (o, m, l) into the running state of the row.
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const float lt = group4_sum(lsum[nb]);
     const int row = qw0 + 16 * nb + c;
     if (row < a.Nq) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const float mnat = (mrun[nb] == -INFINITY) ? -INFINITY : mrun[nb] * kLn2;
       float* orow = a.o + (((int64_t)b * a.Nq + row) * a.Hq + h) * D;
+      const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
+      float wa = 0.f, wb = inv, mo = mnat, lo = lt;
+      if (a.accumulate) {
+        const MergeW w = merge_weights(a.m[si], a.l[si], mnat, lt);
+        wa = w.wa;
+        wb = w.wb * inv;
+        mo = w.m;
+        lo = w.l;
+      }
 #pragma unroll
-      for (int db = 0; db < C::DB; ++db)
-        *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db][nb] * inv;
+      for (int db = 0; db < C::DB; ++db) {
+        f32x4* dst = reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g);
+        *dst = a.accumulate ? *dst * wa + o[db][nb] * wb : o[db][nb] * wb;
+      }
       if (g == 0) {
-        const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
-        a.m[si] = (mrun[nb] == -INFINITY) ? -INFINITY : mrun[nb] * kLn2;
-        a.l[si] = lt;
+        a.m[si] = mo;
+        a.l[si] = lo;
       }
     }
   }
@@ -252,6 +265,7 @@ hipError_t launch_fwd_mfma(const Problem& p, const void* q, const void* k, const
   a.k_pos0 = p.k_pos0;
   a.valid = p.valid;
   a.causal = p.causal ? 1 : 0;
+  a.accumulate = p.accumulate ? 1 : 0;
   a.sl2 = p.scale * kLog2e;
   if (p.D == 128) {
     a.n_qtiles = (p.Nq + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM;

@@ -38,6 +38,7 @@ struct GenArgs {
   int B, Nq, Nk, Hq, Hkv, D, group, n_tiles;
   int64_t q_pos0, k_pos0, valid;
   int causal;
+  int accumulate;  // forward: merge into the running (o, m, l) instead of writing them
   float scale;
 };
 
@@ -142,18 +143,22 @@ __global__ __launch_bounds__(256) void fwd_generic_kernel(GenArgs a) {
     m = mnew;
   }
 
+  // accumulate: LSE-merge (o, m, l) into the running state of the row, with
+  // the arithmetic of lc_attn_merge on the normalised partial.
   if (ok) {
     const float den = l > kFltMin ? l : kFltMin;
     float* orow = a.o + (((int64_t)b * a.Nq + row) * a.Hq + h) * D;
+    const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
+    MergeW w{};
+    if (a.accumulate) w = merge_weights(a.m[si], a.l[si], m, l);
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
       const int d = sub + 4 * jj;
-      if (d < D) orow[d] = acc[jj] / den;
+      if (d < D) orow[d] = a.accumulate ? orow[d] * w.wa + (acc[jj] / den) * w.wb : acc[jj] / den;
     }
     if (sub == 0) {
-      const int64_t si = ((int64_t)b * a.Hq + h) * a.Nq + row;
-      a.m[si] = m;
-      a.l[si] = l;
+      a.m[si] = a.accumulate ? w.m : m;
+      a.l[si] = a.accumulate ? w.l : l;
     }
   }
 }
@@ -357,6 +362,7 @@ GenArgs make_args(const Problem& p) {
   a.k_pos0 = p.k_pos0;
   a.valid = p.valid;
   a.causal = p.causal ? 1 : 0;
+  a.accumulate = p.accumulate ? 1 : 0;
   a.scale = p.scale;
   return a;
 }

@@ -15,7 +15,8 @@ struct Problem {
   int64_t q_pos0, k_pos0;
   int64_t valid;  // INT64_MAX when the reference's valid_length is None
   bool causal;
-  float scale;  // D^-1/2
+  float scale;      // D^-1/2
+  bool accumulate;  // forward: LSE-merge into the running (o, m, l) instead of writing them
 };
 
 // Index of the exclusive end of the keys that any query of [q_begin, q_end)
@@ -38,7 +39,8 @@ bool mfma_supported(const Problem& p);
 // key, p.Nk and p.k_pos0 describe the sub-shard, kv_rows is the key count of
 // the whole shard (the batch stride of K and V; -1: p.Nk), and accumulate
 // merges the result into the running (o, m, l) with the weights of
-// lc_attn_merge instead of overwriting them.
+// lc_attn_merge instead of overwriting them (launch_fwd_mfma and
+// launch_fwd_generic take it from p.accumulate).
 hipError_t launch_fwd128(const Problem& p, const void* q, const void* k, const void* v, float* o,
                          float* m, float* l, hipStream_t s, int64_t kv_rows = -1,
                          bool accumulate = false);

@@ -4,8 +4,9 @@ check, so both run exactly the same launches.
 
 Forward (ring_attention.rs:139-233): the query shard attends the KV shard of
 owner (rank - h) mod world at hop h, fully masked hops skipped; hop 0 writes
-the running state, every later hop's partial is LSE-merged into it and the
-last merge also writes the bf16 output (rs:227-231).
+the running state, every later hop LSE-merges its result into it in the
+forward kernel's epilogue (the carried state of rs:195-225), and a cast
+writes the bf16 output (rs:227-231).
 
 Backward (rs:281-475, one rank's share): the preprocess forms delta from the
 cast output and the log2-domain LSE; then, per visited owner, the hop
@@ -68,9 +69,6 @@ class RankStep:
         self.o_run = torch.empty(b, n, h, d, **f32)
         self.m = torch.empty(b, h, n, **f32)
         self.l = torch.empty(b, h, n, **f32)
-        self.o_part = torch.empty_like(self.o_run)
-        self.m_part = torch.empty_like(self.m)
-        self.l_part = torch.empty_like(self.l)
         self.out = torch.empty(b, n, h, d, device=dev, dtype=q.dtype)
         self.delta = torch.empty_like(self.m)
         self.lse2 = torch.empty_like(self.m)
@@ -96,20 +94,10 @@ class RankStep:
     def forward(self, timed: Optional[Timer] = None) -> None:
         n, qp = self.n, self.q_pos0
         for i, b in enumerate(self.owners):
-            if i == 0:
-                _run(timed, f"fwd_{self.tag(b)}", lambda b=b: ra.fwd_shard(
-                    self.q, self.ks[b], self.vs[b], q_pos0=qp, k_pos0=b * n,
-                    o=self.o_run, m=self.m, l=self.l))
-                continue
-            _run(timed, f"fwd_{self.tag(b)}", lambda b=b: ra.fwd_shard(
+            _run(timed, f"fwd_{self.tag(b)}", lambda b=b, i=i: ra.fwd_shard(
                 self.q, self.ks[b], self.vs[b], q_pos0=qp, k_pos0=b * n,
-                o=self.o_part, m=self.m_part, l=self.l_part))
-            last = i + 1 == len(self.owners)
-            _run(timed, "merge", lambda last=last: ra.merge(
-                self.o_run, self.m, self.l, self.o_part, self.m_part, self.l_part,
-                out=self.out if last else None))
-        if len(self.owners) == 1:
-            ra.cast(self.o_run, self.out)
+                o=self.o_run, m=self.m, l=self.l, accumulate=i > 0))
+        _run(timed, "cast", lambda: ra.cast(self.o_run, self.out))
 
     def backward(self, timed: Optional[Timer] = None) -> None:
         n, qp = self.n, self.q_pos0
@@ -138,8 +126,9 @@ class RankStep:
 
 class LongShardForward:
     """BASELINE config 5's forward: the query shard at rank 1 of a 2-shard
-    layout attends its diagonal KV shard and one full incoming shard, merged
-    by LSE (``out`` bf16, ``m``/``l`` fp32 statistics)."""
+    layout attends its diagonal KV shard and one full incoming shard, whose
+    result the forward LSE-merges into the diagonal's (``out`` bf16, ``m``/``l``
+    fp32 statistics)."""
 
     def __init__(self, q: torch.Tensor, ks: Sequence[torch.Tensor], vs: Sequence[torch.Tensor]):
         self.q, self.ks, self.vs = q, list(ks), list(vs)
@@ -147,18 +136,16 @@ class LongShardForward:
         self.n = n
         f32 = dict(device=q.device, dtype=torch.float32)
         self.o_run = torch.empty(b, n, h, d, **f32)
-        self.o_part = torch.empty(b, n, h, d, **f32)
-        self.m, self.l, self.m_part, self.l_part = (torch.empty(b, h, n, **f32) for _ in range(4))
+        self.m, self.l = (torch.empty(b, h, n, **f32) for _ in range(2))
         self.out = torch.empty(b, n, h, d, device=q.device, dtype=q.dtype)
 
     def resident(self) -> List[torch.Tensor]:
-        return [self.q, *self.ks, *self.vs, self.o_run, self.o_part, self.m, self.l,
-                self.m_part, self.l_part, self.out]
+        return [self.q, *self.ks, *self.vs, self.o_run, self.m, self.l, self.out]
 
     def forward(self) -> None:
         n = self.n
         ra.fwd_shard(self.q, self.ks[1], self.vs[1], q_pos0=n, k_pos0=n,
                      o=self.o_run, m=self.m, l=self.l)                      # diagonal
         ra.fwd_shard(self.q, self.ks[0], self.vs[0], q_pos0=n, k_pos0=0,
-                     o=self.o_part, m=self.m_part, l=self.l_part)           # full shard
-        ra.merge(self.o_run, self.m, self.l, self.o_part, self.m_part, self.l_part, out=self.out)
+                     o=self.o_run, m=self.m, l=self.l, accumulate=True)     # full shard
+        ra.cast(self.o_run, self.out)

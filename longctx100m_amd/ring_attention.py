@@ -75,14 +75,22 @@ def _shape(q: torch.Tensor, k: torch.Tensor, precise: bool) -> _lib.Shape:
 def fwd_shard(q, k, v, *, q_pos0: int, k_pos0: int, causal: bool = True,
               valid_length: Optional[int] = None, precise: bool = False,
               o: Optional[torch.Tensor] = None, m: Optional[torch.Tensor] = None,
-              l: Optional[torch.Tensor] = None):
+              l: Optional[torch.Tensor] = None, accumulate: bool = False):
     """One hop: attention of the query shard over one KV shard.
 
-    Returns (o [B,Nq,Hq,D] fp32 normalised, m [B,Hq,Nq], l [B,Hq,Nq])."""
+    Returns (o [B,Nq,Hq,D] fp32 normalised, m [B,Hq,Nq], l [B,Hq,Nq]).  With
+    ``accumulate`` the given o, m, l hold a running state and the hop's result
+    is LSE-merged into them in the kernel's epilogue (as :func:`merge` would
+    merge a separate partial), the reference's state carried over the hop loop
+    (rs:195-225)."""
     _check_dev(q, k, v)
     if k.shape != v.shape or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, v shard shapes must match")
+    if accumulate and (o is None or m is None or l is None):
+        raise ValueError("accumulate needs the running o, m and l")
     s = _shape(q, k, precise)
+    if accumulate:
+        s.flags |= _lib.LC_FLAG_ACCUMULATE
     b, nq, hq, d = q.shape
     o = torch.empty((b, nq, hq, d), dtype=torch.float32, device=q.device) if o is None else o
     m = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if m is None else m

@@ -85,7 +85,7 @@ def test_workspace_sizes(lib):
     d = _desc(local_tokens=32768, heads_q=16, heads_kv=16, head_dim=128, world=8, rank=7)
     n_o = 32768 * 16 * 128
     n_s = 16 * 32768
-    assert lib.lc_ring_fwd_workspace_bytes(d) == 2 * 4 * n_o + 2 * 4 * n_s
+    assert lib.lc_ring_fwd_workspace_bytes(d) == 4 * n_o  # the running output; m, l are outputs
     assert lib.lc_ring_bwd_workspace_bytes(d) == 3 * 4 * n_o + 2 * 4 * n_s
 
 
@@ -111,6 +111,23 @@ def test_null_and_workspace_errors(lib):
     assert rc == _lib.LC_ERR_UNSUPPORTED
     rc = lib.lc_attn_cast(None, None, 10, 5, None)
     assert rc == _lib.LC_ERR_UNSUPPORTED
+
+
+def test_accumulate_flag_is_for_fwd_shard_only(lib):
+    """LC_FLAG_ACCUMULATE merges a hop into a running state in lc_attn_fwd_shard;
+    the decode entry points and the ring descriptor reject it before any GPU work."""
+    acc = _lib.LC_FLAG_ACCUMULATE
+    msg = "LC_FLAG_ACCUMULATE applies to lc_attn_fwd_shard only"
+    shape = _lib.Shape(1, 1, 4096, 8, 2, 128, _lib.LC_DTYPE_BF16, acc)
+    mask = _lib.Mask(4095, 0, -1, 1, 0)
+    rc = lib.lc_attn_decode(shape, mask, 16, 16, 16, 16, 16, 16, 16, 1 << 20, None)
+    assert rc == _lib.LC_ERR_INVALID and lib.lc_last_error().decode() == msg
+    rc = lib.lc_attn_decode_static(shape, mask, 16, 16, 16, 16, 16, 16, None)
+    assert rc == _lib.LC_ERR_INVALID and lib.lc_last_error().decode() == msg
+    d = _desc(flags=acc)
+    assert lib.lc_ring_fwd_workspace_bytes(d) == 0
+    rc = lib.lc_ring_fwd_with_stats(d, None, None, None, None, None, None, None, 0, None)
+    assert rc == _lib.LC_ERR_INVALID and lib.lc_last_error().decode() == msg
 
 
 def test_last_error_is_per_thread(lib):

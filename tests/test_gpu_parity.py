@@ -348,6 +348,79 @@ def test_merge_is_order_invariant(ra, gpu):
         assert norm_rel(o, results[0][0]) <= 1e-5
 
 
+ACC_CASES = [
+    # b, nq, nk_a, nk_b, hq, hkv, d, dtype, precise, q_pos0, shift, valid: hop A holds
+    # the keys from q_pos0 + shift on, hop B the nk_b keys just before them
+    (1, 300, 300, 300, 4, 2, 128, "bfloat16", False, 600, 0, None),   # diagonal, then full hop
+    (1, 520, 300, 260, 2, 2, 128, "bfloat16", False, 1000, 0, 1100),  # 8-wave hop, valid_length
+    (2, 200, 160, 130, 8, 2, 128, "bfloat16", False, 500, 100, None),  # rows with no key in A
+    (1, 96, 64, 64, 2, 1, 128, "bfloat16", False, 0, 64, None),       # no A key for rows < 64
+    (1, 200, 200, 150, 2, 1, 64, "bfloat16", False, 300, 0, 320),     # d=64 kernel
+    (1, 150, 100, 90, 3, 1, 128, "float32", False, 200, 0, None),     # fp32 kernel
+    (1, 130, 70, 80, 2, 2, 40, "float32", False, 100, 0, None),       # fp32, d=40
+    (1, 120, 100, 100, 2, 1, 128, "bfloat16", True, 150, 0, 180),     # bf16 inputs, fp32 math
+    (1, 48, 64, 70000, 1, 1, 128, "bfloat16", False, 70000, 0, None),  # B over key sub-shards
+]
+
+
+@pytest.mark.parametrize("case", ACC_CASES)
+def test_fwd_accumulate_matches_separate_merge(ra, gpu, case):
+    """LC_FLAG_ACCUMULATE: hop B merged into hop A's state in the forward's
+    epilogue equals hop B into its own buffers followed by lc_attn_merge (m and
+    l bit for bit, o to fp32 rounding; a hop of key sub-shards merges them one
+    by one into A's state instead of into each other first, so l then agrees
+    to fp32 rounding), and both equal the fp64 dense oracle over the union of
+    the two hops' keys."""
+    b, nq, nka, nkb, hq, hkv, d, dt, precise, qp, shift, valid = case
+    dtype = getattr(gpu, dt)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    q = _t(gpu, rng.standard_normal((b, nq, hq, d)), dtype)
+    ka, va, kb, vb = (_t(gpu, rng.standard_normal((b, n, hkv, d)), dtype)
+                      for n in (nka, nka, nkb, nkb))
+    kpa = qp + shift  # hop A's first key position
+    kpb = kpa - nkb
+    kw = dict(valid_length=valid, precise=precise)
+    o_a, m_a, l_a = ra.fwd_shard(q, ka, va, q_pos0=qp, k_pos0=kpa, **kw)
+    o_b, m_b, l_b = ra.fwd_shard(q, kb, vb, q_pos0=qp, k_pos0=kpb, **kw)
+    sep = [x.clone() for x in (o_a, m_a, l_a)]
+    ra.merge(*sep, o_b, m_b, l_b)
+    acc = [x.clone() for x in (o_a, m_a, l_a)]
+    ra.fwd_shard(q, kb, vb, q_pos0=qp, k_pos0=kpb, o=acc[0], m=acc[1], l=acc[2],
+                 accumulate=True, **kw)
+    gpu.cuda.synchronize()
+    (so, sm, sl), (ao, am, al) = ([_np(x) for x in t] for t in (sep, acc))
+    assert np.array_equal(am, sm)
+    if nkb <= 65536:
+        assert np.array_equal(al, sl)
+    else:
+        assert np.abs(al - sl).max() <= 1e-6 * np.abs(sl).max()
+    assert np.abs(ao - so).max() <= 1e-6 * max(np.abs(so).max(), 1e-30)
+    kcat = np.concatenate([_np(kb), _np(ka)], axis=1)
+    vcat = np.concatenate([_np(vb), _np(va)], axis=1)
+    eo, em, el = dense.attention_fwd(_np(q), kcat, vcat, q_pos0=qp, k_pos0=kpb,
+                                     valid_length=valid)
+    tol = FP32_TOL if (dt == "float32" or precise) else BF16_TOL
+    assert norm_rel(ao, eo) <= tol
+    fin = np.isfinite(em)
+    assert np.array_equal(np.isfinite(am), fin)
+    assert np.abs(am[fin] - em[fin]).max() <= 1e-4 * max(np.abs(em[fin]).max(), 1.0)
+    assert norm_rel(al, el) <= 1e-4
+
+
+def test_fwd_accumulate_masked_pair_keeps_state(ra, gpu):
+    """A hop with no unmasked pair leaves an accumulated state as it is (the
+    reference's alpha = 1, p = 0), where a write would reset it."""
+    rng = np.random.default_rng(11)
+    q = _t(gpu, rng.standard_normal((1, 64, 2, 128)), gpu.bfloat16)
+    k, v = (_t(gpu, rng.standard_normal((1, 64, 2, 128)), gpu.bfloat16) for _ in range(2))
+    o, m, l = ra.fwd_shard(q, k, v, q_pos0=100, k_pos0=0)
+    before = [_np(x) for x in (o, m, l)]
+    ra.fwd_shard(q, k, v, q_pos0=100, k_pos0=500, o=o, m=m, l=l, accumulate=True)  # keys after
+    gpu.cuda.synchronize()
+    for x, y in zip(before, (o, m, l)):
+        assert np.array_equal(x, _np(y))
+
+
 # ------------------------------------------------------------------ whole ring --
 
 def _oracle_ring(qs, ks, vs, world, hq, hkv, rank=None, gos=None, **kw):
