@@ -182,12 +182,18 @@ class ClockSampler:
         if self._thread is not None:
             self._thread.join()
 
+    # Readings below this are not the clock of a GPU busy with these kernels (under
+    # rocprofv3 most readings come back at the 158 MHz idle level): they are dropped,
+    # and with fewer than half the readings left there is no summary.
+    MIN_BUSY_MHZ = 500.0
+
     def summary(self):
-        if not self.samples:
+        xs = [x for x in self.samples if x >= self.MIN_BUSY_MHZ]
+        if not xs or 2 * len(xs) < len(self.samples):
             return None
-        xs = self.samples
         return {"mean": round(sum(xs) / len(xs), 1), "median": sorted(xs)[len(xs) // 2],
-                "min": min(xs), "max": max(xs), "samples": len(xs)}
+                "min": min(xs), "max": max(xs), "samples": len(xs),
+                "dropped_below_500": len(self.samples) - len(xs)}
 
 
 def measured_traffic(rl_kernel: str, n: int, h: int, d: int):

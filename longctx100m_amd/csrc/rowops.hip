@@ -97,6 +97,21 @@ __global__ void cast_kernel(int64_t n, const float* src, T* dst) {
     store_from_f32(dst + i, src[i]);
 }
 
+// fp32 -> bf16, eight elements per lane: two 16-byte loads, one 16-byte store
+// (n8 = n / 8; both pointers 16-byte aligned).  Same rounding as cast_kernel.
+__global__ void cast_bf16x8_kernel(int64_t n8, const f32x4* src, uint4* dst) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const f32x4 a = src[2 * i], b = src[2 * i + 1];
+    uint4 r;
+    r.x = (uint32_t)f32_to_bf16(a[0]) | ((uint32_t)f32_to_bf16(a[1]) << 16);
+    r.y = (uint32_t)f32_to_bf16(a[2]) | ((uint32_t)f32_to_bf16(a[3]) << 16);
+    r.z = (uint32_t)f32_to_bf16(b[0]) | ((uint32_t)f32_to_bf16(b[1]) << 16);
+    r.w = (uint32_t)f32_to_bf16(b[2]) | ((uint32_t)f32_to_bf16(b[3]) << 16);
+    dst[i] = r;
+  }
+}
+
 // delta = rowsum(dout * out) over D (both in the input dtype, upcast to fp32),
 // lse2 = m*log2(e) + log2(max(l, FLT_MIN)), +inf where m = -inf so that
 // 2^(s*log2e - lse2) = 0 for rows that saw no key.  A group of 16 lanes owns
@@ -197,7 +212,12 @@ hipError_t launch_init_state(int B, int N, int H, int D, float* o, float* m, flo
 }
 
 hipError_t launch_cast(const float* src, void* dst, int64_t n, int dtype, hipStream_t s) {
-  if (dtype == 1)
+  const bool vec = n % 8 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+  if (dtype == 1 && vec)
+    hipLaunchKernelGGL(cast_bf16x8_kernel, grid_for(n / 8), dim3(256), 0, s, n / 8,
+                       reinterpret_cast<const f32x4*>(src), static_cast<uint4*>(dst));
+  else if (dtype == 1)
     hipLaunchKernelGGL(cast_kernel<uint16_t>, grid_for(n), dim3(256), 0, s, n, src,
                        static_cast<uint16_t*>(dst));
   else

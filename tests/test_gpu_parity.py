@@ -324,6 +324,31 @@ def test_bwd_shard_shared_ds(ra, gpu, case):
     assert norm_rel(dv, edv) <= BF16_TOL
 
 
+@pytest.mark.parametrize("n,offset", [(8 * 40000, 0), (8 * 40000 + 3, 0), (8 * 1000, 1)])
+def test_cast_rounds_to_nearest_even(ra, gpu, n, offset):
+    """lc_attn_cast to bf16 (the 8-wide kernel for aligned multiples of 8, the
+    scalar one otherwise) rounds to nearest even, bit for bit as torch's CPU
+    conversion, including ties, subnormals, infinities and NaN."""
+    rng = np.random.default_rng(n + offset)
+    bits = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+    bits[: n // 4] = (bits[: n // 4] & 0xFFFF0000) | 0x8000  # exact ties
+    special = np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0x00000001, 0x807FFFFF,
+                        0x3F808000, 0x3F818000, 0x7F7FFFFF], dtype=np.uint32)
+    bits[-len(special):] = special
+    src_cpu = gpu.from_numpy(bits.view(np.float32).copy())
+    src = src_cpu.cuda()
+    dst_full = gpu.empty(n + offset, dtype=gpu.bfloat16, device="cuda")
+    dst = dst_full[offset:]
+    ra.cast(src, dst)
+    gpu.cuda.synchronize()
+    got = dst.cpu().view(gpu.int16).numpy()
+    exp_t = src_cpu.to(gpu.bfloat16)
+    exp = exp_t.view(gpu.int16).numpy()
+    nan = np.isnan(src_cpu.numpy())
+    assert np.array_equal(got[~nan], exp[~nan])
+    assert np.isnan(dst.cpu().float().numpy()[nan]).all()
+
+
 def test_merge_is_order_invariant(ra, gpu):
     rng = np.random.default_rng(5)
     nq, hq, d = 192, 2, 128
