@@ -499,6 +499,65 @@ def test_ring_config1(ra, gpu, dtype_name):
             assert norm_rel(_np(a), b) <= tol
 
 
+def _random_rings(seed, n):
+    """Random ring geometries (drawn once): world, rank, shard length, heads, d,
+    dtype, causal, valid_length, q_position_start."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        world = int(rng.integers(1, 5))
+        tokens = int(rng.integers(1, 261))
+        dt = str(rng.choice(["float32", "bfloat16"]))
+        hkv = int(rng.integers(1, 3))
+        valid = None if rng.integers(0, 2) else int(rng.integers(1, world * tokens + 1))
+        qps = None if rng.integers(0, 3) else int(rng.integers(0, world * tokens))
+        out.append(dict(world=world, rank=int(rng.integers(0, world)), n=tokens, hkv=hkv,
+                        hq=hkv * int(rng.integers(1, 4)), dtype=dt,
+                        d=int(rng.choice([64, 128] if dt == "bfloat16" else [40, 64, 128])),
+                        causal=bool(rng.integers(0, 4)), valid_length=valid,
+                        q_position_start=qps))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_rings(2027, 32),
+                         ids=lambda c: "w{world}r{rank}n{n}h{hq}/{hkv}d{d}-{dtype}".format(**c))
+def test_random_rings_against_the_c_restatement(ra, gpu, case):
+    """Whole-ring forward and backward of one rank through the C ABI (the
+    reference's signatures) against the C restatement of rs:139-475 on the same
+    inputs, at the fp32 / bf16 bars: random world sizes, ranks, shard lengths
+    that are not multiples of any tile, GQA, head dims, causal or not,
+    valid_length and q_position_start."""
+    c = dict(case)
+    dtype = getattr(gpu, c["dtype"])
+    tol = FP32_TOL if c["dtype"] == "float32" else BF16_TOL
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    world, rank, n, hq, hkv, d = c["world"], c["rank"], c["n"], c["hq"], c["hkv"], c["d"]
+    kw = dict(causal=c["causal"], valid_length=c["valid_length"],
+              q_position_start=c["q_position_start"])
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, hq, hkv, d, dtype)
+    gos = [_t(gpu, rng.standard_normal((1, n, hq, d)), dtype) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    fw = [ra.ring_causal_attention_forward_with_stats(shards, r, c["causal"], 64, 128,
+                                                      c["valid_length"], c["q_position_start"])
+          for r in range(world)]
+    outs, ms, ls = (list(x) for x in zip(*fw))
+    dq, dk, dv = ra.ring_causal_attention_backward(shards, rank, outs, ms, ls, gos, c["causal"],
+                                                   64, 128, c["valid_length"],
+                                                   c["q_position_start"])
+    gpu.cuda.synchronize()
+    efw, egrads = _oracle_ring(qs, ks, vs, world, hq, hkv, rank=rank, gos=gos, **kw)
+    eo, em, el = efw[rank]
+    assert norm_rel(_np(outs[rank]), eo) <= tol
+    m, l = _np(ms[rank])[..., 0], _np(ls[rank])[..., 0]
+    fin = np.isfinite(em)
+    assert np.array_equal(np.isfinite(m), fin)
+    if fin.any():
+        assert np.abs(m[fin] - em[fin]).max() <= 1e-4 * max(np.abs(em[fin]).max(), 1.0)
+        assert norm_rel(l, el) <= 1e-4
+    for a, e in zip((dq, dk, dv), egrads):
+        assert norm_rel(_np(a), e) <= tol
+
+
 def test_reference_unit_cases_on_gpu(ra, gpu):
     """The reference's Rust unit tests (ring_attention.rs:519-668) through
     the HIP path, fp32, same shapes, blocks and tolerances."""
