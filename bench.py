@@ -75,6 +75,10 @@ def parse():
     ap.add_argument("--bwd-recompute", action="store_true",
                     help="backward without dS sharing: the dQ kernel recomputes S and dP "
                          "instead of reading the dS the dK/dV kernel stored")
+    ap.add_argument("--separate-merge", action="store_true",
+                    help="forward with each later hop into its own partial buffers and the "
+                         "lc_attn_merge kernel per hop, instead of the merge in the forward's "
+                         "epilogue (measures the merge kernel's HBM rate in the step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -625,7 +629,8 @@ def main() -> int:
     dout = randn(1, n, h, d)
     ks = [randn(1, n, h, d) for _ in range(world)]
     vs = [randn(1, n, h, d) for _ in range(world)]
-    rs = RankStep(q, dout, ks, vs, rank, share_ds=not args.bwd_recompute)
+    rs = RankStep(q, dout, ks, vs, rank, share_ds=not args.bwd_recompute,
+                  separate_merge=args.separate_merge)
     owners = rs.owners
     ws = rs.workspace
     if ws is not None:
@@ -737,7 +742,8 @@ def main() -> int:
         "config": {
             "workload": (f"BASELINE configs 2+3: rank {rank} of {world}, {n}-token bf16 local "
                          f"shard, Hq=Hkv={h}, d={d}; fwd over diagonal + {n_full} full KV shards "
-                         f"with LSE merge, then recompute bwd (dQ across shards, dK/dV per "
+                         f"with LSE merge" + (" (merge kernel per hop)" if args.separate_merge
+                                              else "") + ", then recompute bwd (dQ across shards, dK/dV per "
                          f"shard; " + ("dS shared by the dK/dV and dQ kernels)" if ws is not None
                                        else "dQ kernel recomputes dS)")),
             "world": world, "rank": rank, "local_tokens": n, "heads_q": h, "heads_kv": h,

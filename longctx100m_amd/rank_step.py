@@ -6,7 +6,9 @@ Forward (ring_attention.rs:139-233): the query shard attends the KV shard of
 owner (rank - h) mod world at hop h, fully masked hops skipped; hop 0 writes
 the running state, every later hop LSE-merges its result into it in the
 forward kernel's epilogue (the carried state of rs:195-225), and a cast
-writes the bf16 output (rs:227-231).
+writes the bf16 output (rs:227-231); with ``separate_merge`` each later hop
+writes its own partial and lc_attn_merge merges it, the last merge also
+writing the bf16 output.
 
 Backward (rs:281-475, one rank's share): the preprocess forms delta from the
 cast output and the log2-domain LSE; then, per visited owner, the hop
@@ -58,7 +60,7 @@ class RankStep:
 
     def __init__(self, q: torch.Tensor, dout: torch.Tensor, ks: Sequence[torch.Tensor],
                  vs: Sequence[torch.Tensor], rank: int, *, share_ds: bool = True,
-                 workspace_bytes: Optional[int] = None):
+                 workspace_bytes: Optional[int] = None, separate_merge: bool = False):
         self.q, self.dout, self.ks, self.vs, self.rank = q, dout, list(ks), list(vs), rank
         b, n, h, d = q.shape
         self.n = n
@@ -70,6 +72,11 @@ class RankStep:
         self.m = torch.empty(b, h, n, **f32)
         self.l = torch.empty(b, h, n, **f32)
         self.out = torch.empty(b, n, h, d, device=dev, dtype=q.dtype)
+        self.separate_merge = separate_merge
+        if separate_merge:  # each later hop's partial, merged by lc_attn_merge
+            self.o_part = torch.empty_like(self.o_run)
+            self.m_part = torch.empty_like(self.m)
+            self.l_part = torch.empty_like(self.l)
         self.delta = torch.empty_like(self.m)
         self.lse2 = torch.empty_like(self.m)
         hkv = self.ks[0].shape[2]
@@ -93,6 +100,21 @@ class RankStep:
 
     def forward(self, timed: Optional[Timer] = None) -> None:
         n, qp = self.n, self.q_pos0
+        if self.separate_merge:
+            for i, b in enumerate(self.owners):
+                dst = (self.o_run, self.m, self.l) if i == 0 else (self.o_part, self.m_part,
+                                                                   self.l_part)
+                _run(timed, f"fwd_{self.tag(b)}", lambda b=b, dst=dst: ra.fwd_shard(
+                    self.q, self.ks[b], self.vs[b], q_pos0=qp, k_pos0=b * n,
+                    o=dst[0], m=dst[1], l=dst[2]))
+                if i > 0:
+                    last = i + 1 == len(self.owners)
+                    _run(timed, "merge", lambda last=last: ra.merge(
+                        self.o_run, self.m, self.l, self.o_part, self.m_part, self.l_part,
+                        out=self.out if last else None))
+            if len(self.owners) == 1:
+                ra.cast(self.o_run, self.out)
+            return
         for i, b in enumerate(self.owners):
             _run(timed, f"fwd_{self.tag(b)}", lambda b=b, i=i: ra.fwd_shard(
                 self.q, self.ks[b], self.vs[b], q_pos0=qp, k_pos0=b * n,

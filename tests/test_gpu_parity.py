@@ -432,6 +432,36 @@ def test_fwd_accumulate_matches_separate_merge(ra, gpu, case):
     assert norm_rel(al, el) <= 1e-4
 
 
+def test_rank_step_merge_forms_agree(ra, gpu):
+    """The benched step's forward with the epilogue merge and with a separate
+    lc_attn_merge per hop (bench.py --separate-merge): the same m and l bit for
+    bit, the bf16 output to its rounding, and both at the bf16 bar of the dense
+    oracle over the whole visible sequence."""
+    from longctx100m_amd.rank_step import RankStep
+
+    rng = np.random.default_rng(23)
+    world, rank, n, h, d = 4, 3, 300, 2, 128
+    q = _t(gpu, rng.standard_normal((1, n, h, d)), gpu.bfloat16)
+    do = _t(gpu, rng.standard_normal((1, n, h, d)), gpu.bfloat16)
+    ks = [_t(gpu, rng.standard_normal((1, n, h, d)), gpu.bfloat16) for _ in range(world)]
+    vs = [_t(gpu, rng.standard_normal((1, n, h, d)), gpu.bfloat16) for _ in range(world)]
+    res = []
+    for sep in (False, True):
+        rs = RankStep(q, do, ks, vs, rank, share_ds=False, separate_merge=sep)
+        rs.forward()
+        gpu.cuda.synchronize()
+        res.append((_np(rs.out), _np(rs.m), _np(rs.l)))
+    (fo, fm, fl), (so, sm, sl) = res
+    assert np.array_equal(fm, sm) and np.array_equal(fl, sl)
+    assert norm_rel(fo, so) <= 8e-3
+    kcat = np.concatenate([_np(x) for x in ks], axis=1)
+    vcat = np.concatenate([_np(x) for x in vs], axis=1)
+    eo, em, el = dense.attention_fwd(_np(q), kcat, vcat, q_pos0=rank * n, k_pos0=0)
+    for o in (fo, so):
+        assert norm_rel(o, eo) <= BF16_TOL
+    assert norm_rel(fl, el) <= 1e-4
+
+
 def test_fwd_accumulate_masked_pair_keeps_state(ra, gpu):
     """A hop with no unmasked pair leaves an accumulated state as it is (the
     reference's alpha = 1, p = 0), where a write would reset it."""
