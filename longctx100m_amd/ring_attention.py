@@ -51,6 +51,17 @@ def _check_dev(*ts: torch.Tensor) -> None:
             raise ValueError("tensors must be contiguous")
 
 
+def _check_buf(t: Optional[torch.Tensor], shape, name: str, dtype=torch.float32) -> None:
+    """A caller-supplied output or state buffer must have exactly the shape and
+    dtype the kernels index (they take raw device pointers)."""
+    if t is None:
+        return
+    _check_dev(t)
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+        raise ValueError(f"{name} must be a {dtype} tensor of shape {tuple(shape)}, "
+                         f"got {t.dtype} {tuple(t.shape)}")
+
+
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -92,6 +103,9 @@ def fwd_shard(q, k, v, *, q_pos0: int, k_pos0: int, causal: bool = True,
     if accumulate:
         s.flags |= _lib.LC_FLAG_ACCUMULATE
     b, nq, hq, d = q.shape
+    _check_buf(o, (b, nq, hq, d), "o")
+    _check_buf(m, (b, hq, nq), "m")
+    _check_buf(l, (b, hq, nq), "l")
     o = torch.empty((b, nq, hq, d), dtype=torch.float32, device=q.device) if o is None else o
     m = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if m is None else m
     l = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if l is None else l
@@ -111,6 +125,9 @@ def decode(q, k, v, *, q_pos0: int, k_pos0: int = 0, causal: bool = True,
     s = _shape(q, k, False)
     mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
     b, nq, hq, d = q.shape
+    _check_buf(o, (b, nq, hq, d), "o")
+    _check_buf(m, (b, hq, nq), "m")
+    _check_buf(l, (b, hq, nq), "l")
     o = torch.empty((b, nq, hq, d), dtype=torch.float32, device=q.device) if o is None else o
     m = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if m is None else m
     l = torch.empty_like(m) if l is None else l
@@ -129,6 +146,12 @@ def merge(o_run, m_run, l_run, o_part, m_part, l_part, out: Optional[torch.Tenso
     also writes the merged output cast to ``out``'s dtype."""
     _check_dev(o_run, m_run, l_run, o_part, m_part, l_part)
     b, nq, hq, d = o_run.shape
+    _check_buf(o_run, (b, nq, hq, d), "o_run")
+    _check_buf(o_part, (b, nq, hq, d), "o_part")
+    for name, t in (("m_run", m_run), ("l_run", l_run), ("m_part", m_part), ("l_part", l_part)):
+        _check_buf(t, (b, hq, nq), name)
+    if out is not None:
+        _check_buf(out, (b, nq, hq, d), "out", out.dtype)
     dt = _lib.LC_DTYPE_F32 if out is None else _dtype_code(out)
     s = _lib.Shape(b, nq, nq, hq, hq, d, dt, 0)
     _lib.check(_lib.load().lc_attn_merge(s, o_run.data_ptr(), m_run.data_ptr(), l_run.data_ptr(),
@@ -149,6 +172,9 @@ def bwd_preprocess(out, dout, m, l, delta=None, lse2=None):
     """delta = rowsum(dout * out), lse2 = m*log2(e) + log2(max(l, FLT_MIN))."""
     _check_dev(out, dout, m, l)
     b, nq, hq, d = out.shape
+    _check_buf(dout, (b, nq, hq, d), "dout", out.dtype)
+    for name, t in (("m", m), ("l", l), ("delta", delta), ("lse2", lse2)):
+        _check_buf(t, (b, hq, nq), name)
     delta = torch.empty((b, hq, nq), dtype=torch.float32, device=out.device) if delta is None else delta
     lse2 = torch.empty_like(delta) if lse2 is None else lse2
     s = _lib.Shape(b, nq, nq, hq, hq, d, _dtype_code(out), 0)
@@ -168,6 +194,14 @@ def bwd_shard(q, k, v, dout, lse2, delta, *, q_pos0: int, k_pos0: int, causal: b
     computed from it instead of recomputing the scores."""
     _check_dev(q, k, v, dout, lse2, delta)
     s = _shape(q, k, precise)
+    b, nq, hq, d = q.shape
+    nk, hkv = k.shape[1], k.shape[2]
+    _check_buf(dout, (b, nq, hq, d), "dout", q.dtype)
+    _check_buf(lse2, (b, hq, nq), "lse2")
+    _check_buf(delta, (b, hq, nq), "delta")
+    _check_buf(dq_acc, (b, nq, hq, d), "dq_acc")
+    _check_buf(dk_acc, (b, nk, hkv, d), "dk_acc")
+    _check_buf(dv_acc, (b, nk, hkv, d), "dv_acc")
     mk = _lib.Mask(q_pos0, k_pos0, _opt(valid_length), int(causal), 0)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     args = (s, mk, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(), lse2.data_ptr(),

@@ -462,6 +462,30 @@ def test_rank_step_merge_forms_agree(ra, gpu):
     assert norm_rel(fl, el) <= 1e-4
 
 
+def test_wrappers_reject_mis_sized_buffers(ra, gpu):
+    """The kernels take raw pointers, so the Python mirror checks every
+    caller-supplied output or state buffer before a launch could write past it."""
+    bf, f32 = gpu.bfloat16, gpu.float32
+    q = gpu.zeros((1, 64, 4, 128), dtype=bf, device="cuda")
+    k = gpu.zeros((1, 80, 2, 128), dtype=bf, device="cuda")
+    good_o = gpu.zeros((1, 64, 4, 128), dtype=f32, device="cuda")
+    stats = gpu.zeros((1, 4, 64), dtype=f32, device="cuda")
+    with pytest.raises(ValueError, match="o must be"):
+        ra.fwd_shard(q, k, k, q_pos0=0, k_pos0=0, o=good_o[:, :32], m=stats, l=stats)
+    with pytest.raises(ValueError, match="m must be"):
+        ra.fwd_shard(q, k, k, q_pos0=0, k_pos0=0, o=good_o, m=stats[:, :2], l=stats,
+                     accumulate=True)
+    with pytest.raises(ValueError, match="accumulate needs"):
+        ra.fwd_shard(q, k, k, q_pos0=0, k_pos0=0, accumulate=True)
+    with pytest.raises(ValueError, match="dk_acc must be"):
+        ra.bwd_shard(q, k, k, q, stats, stats, q_pos0=0, k_pos0=0, dq_acc=good_o,
+                     dk_acc=gpu.zeros((1, 64, 2, 128), dtype=f32, device="cuda"),
+                     dv_acc=gpu.zeros((1, 80, 2, 128), dtype=f32, device="cuda"))
+    with pytest.raises(ValueError, match="o_part must be"):
+        ra.merge(good_o, stats, stats, good_o.to(bf), stats, stats)
+    gpu.cuda.synchronize()
+
+
 def test_fwd_accumulate_masked_pair_keeps_state(ra, gpu):
     """A hop with no unmasked pair leaves an accumulated state as it is (the
     reference's alpha = 1, p = 0), where a write would reset it."""
