@@ -33,6 +33,18 @@ def _chk_cuda(*ts):
             raise ValueError("tensors must live on the GPU (device pointers are passed to HIP)")
 
 
+def _chk_out(t: Optional[torch.Tensor], rows: int, cols: int, dtype, name: str) -> None:
+    """A caller-supplied output of ``rows`` rows of ``cols`` contiguous elements
+    (row stride free): the kernels take raw pointers and write every row."""
+    if t is None:
+        return
+    _chk_cuda(t)
+    if t.dtype != dtype or t.numel() == 0 or t.shape[-1] != cols or t.stride(-1) != 1 or \
+            t.reshape(-1, cols).shape[0] != rows:
+        raise ValueError(f"{name} must be a {dtype} tensor of {rows} rows of {cols} "
+                         f"contiguous elements, got {t.dtype} {tuple(t.shape)}")
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             residual: Optional[torch.Tensor] = None, residual_out: Optional[torch.Tensor] = None,
             out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -43,6 +55,11 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     x2 = x.reshape(-1, cols)
     if x2.stride(-1) != 1:
         raise ValueError("rows must be contiguous")
+    if weight.numel() != cols or weight.dtype != x.dtype:
+        raise ValueError(f"weight must hold {cols} elements of {x.dtype}")
+    _chk_out(residual, x2.shape[0], cols, x.dtype, "residual")
+    _chk_out(residual_out, x2.shape[0], cols, x.dtype, "residual_out")
+    _chk_out(out, x2.shape[0], cols, x.dtype, "out")
     out = torch.empty(x2.shape, dtype=x.dtype, device=x.device) if out is None else out
     r2 = residual.reshape(-1, cols) if residual is not None else None
     ro = residual_out.reshape(-1, cols) if residual_out is not None else None
@@ -104,6 +121,12 @@ def rope_apply(src: torch.Tensor, table: torch.Tensor, heads: int, head_dim: int
     tokens = src.shape[0]
     if src.dim() != 2 or src.shape[1] != heads * head_dim or src.stride(1) != 1:
         raise ValueError("src must be [tokens, heads*head_dim] with contiguous rows")
+    if table.dtype != torch.float32 or table.dim() != 3 or table.shape[0] < tokens or \
+            table.shape[1:] != (2, head_dim // 2) or not table.is_contiguous():
+        raise ValueError("table must be a contiguous [tokens, 2, head_dim/2] fp32 rope_table")
+    if out is not None and (not out.is_contiguous() or out.numel() != tokens * heads * head_dim):
+        raise ValueError("out must be a contiguous [tokens, heads, head_dim] tensor")
+    _chk_out(out, tokens * heads, head_dim, src.dtype, "out")
     out = torch.empty((tokens, heads, head_dim), dtype=src.dtype, device=src.device) \
         if out is None else out
     _lib.check(_lib.load().lc_rope_apply(_dtype_code(src), tokens, heads, head_dim,
@@ -118,6 +141,9 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
     rows, cols = gate.shape
     if up.shape != gate.shape or gate.stride(1) != 1 or up.stride(1) != 1:
         raise ValueError("gate and up must be [rows, cols] with contiguous rows")
+    if out is not None and (not out.is_contiguous() or out.numel() != rows * cols):
+        raise ValueError("out must be a contiguous [rows, cols] tensor")
+    _chk_out(out, rows, cols, gate.dtype, "out")
     out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device) if out is None else out
     _lib.check(_lib.load().lc_swiglu(_dtype_code(gate), rows, cols, gate.data_ptr(),
                                      gate.stride(0), up.data_ptr(), up.stride(0),

@@ -230,3 +230,27 @@ def test_gemv_single_token(ly, gpu, rows, cols, stride):
     bound = 2.0 ** -8 * np.abs(want) + 2.0 ** -22 * cols * np.abs(prod).sum(axis=1)[None, :]
     assert got.shape == (1, rows)
     assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
+def test_wrappers_reject_mis_sized_buffers(ly, gpu):
+    """The layer kernels take raw pointers: the wrappers check caller-supplied
+    outputs, residuals, weights and tables before a launch could overrun them."""
+    bf = gpu.bfloat16
+    x = gpu.zeros((8, 256), dtype=bf, device="cuda")
+    w = gpu.ones(256, dtype=bf, device="cuda")
+    with pytest.raises(ValueError, match="residual_out must be"):
+        ly.rmsnorm(x, w, 1e-5, residual=x, residual_out=gpu.zeros((4, 256), dtype=bf, device="cuda"))
+    with pytest.raises(ValueError, match="weight must hold"):
+        ly.rmsnorm(x, w[:128], 1e-5)
+    with pytest.raises(ValueError, match="out must be"):
+        ly.rmsnorm(x, w, 1e-5, out=gpu.zeros((8, 256), dtype=gpu.float32, device="cuda"))
+    table = ly.rope_table(ly.rope_params(64, 5e5), 8, 0)
+    src = gpu.zeros((8, 2 * 64), dtype=bf, device="cuda")
+    with pytest.raises(ValueError, match="out must be"):
+        ly.rope_apply(src, table, 2, 64, out=gpu.zeros((4, 2, 64), dtype=bf, device="cuda"))
+    with pytest.raises(ValueError, match="table must be"):
+        ly.rope_apply(src, table[:4], 2, 64)
+    gate = gpu.zeros((4, 32), dtype=bf, device="cuda")
+    with pytest.raises(ValueError, match="out must be"):
+        ly.swiglu(gate, gate, out=gpu.zeros((4, 16), dtype=bf, device="cuda"))
+    gpu.cuda.synchronize()
