@@ -217,64 +217,77 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   }
 }
 
-// Log-sum-exp merge of the S split partials of each row: one 256-thread
-// workgroup per row (b, i, h) = ((b * Nq) + i) * Hq + h of o.  The split
-// weights w_s = l_s * exp(m_s - M) are formed in parallel over the splits,
-// then thread (d, half) sums w_s * o_s[d] over half of the splits, so the
-// partial reads are independent and stream.  m and l are written in the
-// [B, Hq, Nq] layout of the statistics.
+// Log-sum-exp merge of the S split partials of each row: one 1024-thread
+// workgroup per row (b, i, h) = ((b * Nq) + i) * Hq + h of o.  A decode step
+// has only B * Nq * Hq rows, too few workgroups to hide latency, so the
+// kernel keeps its chains short: one round of statistics loads (each thread
+// holds the (m, l) of up to four splits), the max M and the sum L of the
+// split weights w_s = l_s * exp(m_s - M) reduced by wave shuffles and one LDS
+// exchange each, then thread (d, g) sums w_s * o_s[d] over the splits
+// s = g mod 8 and the eight group sums meet in LDS.  m and l are written in
+// the [B, Hq, Nq] layout of the statistics.
 constexpr int kMergeMaxSplits = 4096;
+constexpr int kMergeThreads = 1024;
+constexpr int kMergePer = kMergeMaxSplits / kMergeThreads;  // splits per thread
+constexpr int kMergeWaves = kMergeThreads / 64;
+constexpr int kMergeGroups = kMergeThreads / D;
 
-__global__ __launch_bounds__(256) void decode_merge_kernel(int64_t nrows, int S, int Nq, int Hq,
-                                                           const float* o_part,
-                                                           const float* m_part,
-                                                           const float* l_part, float* o,
-                                                           float* m, float* l) {
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    int64_t nrows, int S, int Nq, int Hq, const float* o_part, const float* m_part,
+    const float* l_part, float* o, float* m, float* l) {
   __shared__ float w[kMergeMaxSplits];
-  __shared__ float red[256];
-  __shared__ float half_acc[D];
+  __shared__ float wave_max[kMergeWaves];
+  __shared__ float wave_sum[kMergeWaves];
+  __shared__ float part[kMergeThreads];
   const int t = threadIdx.x;
+  const int wave = t >> 6;
   const int64_t row = blockIdx.x;
-  // M = max over splits
+  float ms[kMergePer], ls[kMergePer];
   float mx = -INFINITY;
-  for (int s = t; s < S; s += 256) mx = fmaxf(mx, m_part[(int64_t)s * nrows + row]);
-  red[t] = mx;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) red[t] = fmaxf(red[t], red[t + off]);
-    __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kMergePer; ++i) {
+    const int sp = t + i * kMergeThreads;
+    ms[i] = sp < S ? m_part[(int64_t)sp * nrows + row] : -INFINITY;
+    ls[i] = sp < S ? l_part[(int64_t)sp * nrows + row] : 0.f;
+    mx = fmaxf(mx, ms[i]);
   }
-  const float M = red[0];
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((t & 63) == 0) wave_max[wave] = mx;
   __syncthreads();
-  // weights and L
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kMergeWaves; ++i) M = fmaxf(M, wave_max[i]);
   float lsum = 0.f;
-  for (int s = t; s < S; s += 256) {
-    const int64_t pr = (int64_t)s * nrows + row;
-    const float ls = l_part[pr];
-    const float ws = (M == -INFINITY || !(ls > 0.f)) ? 0.f : ls * expf(m_part[pr] - M);
-    w[s] = ws;
+#pragma unroll
+  for (int i = 0; i < kMergePer; ++i) {
+    const int sp = t + i * kMergeThreads;
+    const float ws = (M == -INFINITY || !(ls[i] > 0.f)) ? 0.f : ls[i] * expf(ms[i] - M);
+    if (sp < S) w[sp] = ws;
     lsum += ws;
   }
-  red[t] = lsum;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) red[t] += red[t + off];
-    __syncthreads();
-  }
-  const float L = red[0];
-  // weighted sum of the partial outputs: thread (d, half)
+  for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
+  if ((t & 63) == 0) wave_sum[wave] = lsum;
+  __syncthreads();  // w[] and the wave sums are complete
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMergeWaves; ++i) L += wave_sum[i];
+  // weighted sum of the partial outputs: thread (d, g) over splits g, g + 8, ...
   const int d = t & (D - 1);
-  const int hf = t >> 7;  // 0 or 1
+  const int g = t / D;
   float acc = 0.f;  // partials of empty splits are zeros with zero weight
   const float* op = o_part + row * D + d;
-  const int64_t sstride = 2 * nrows * D;
-#pragma unroll 8
-  for (int s = hf; s < S; s += 2) acc = fmaf(w[s], op[(int64_t)(s >> 1) * sstride + (int64_t)hf * nrows * D], acc);
-  if (hf == 1) half_acc[d] = acc;
+  const int64_t sstride = (int64_t)kMergeGroups * nrows * D;
+#pragma unroll 4
+  for (int sp = g; sp < S; sp += kMergeGroups)
+    acc = fmaf(w[sp], op[(int64_t)(sp / kMergeGroups) * sstride + (int64_t)g * nrows * D], acc);
+  part[t] = acc;
   __syncthreads();
-  if (hf == 0) {
+  if (g == 0) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeGroups; ++i) sum += part[i * D + d];
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    o[row * D + d] = (acc + half_acc[d]) * inv;
+    o[row * D + d] = sum * inv;
   }
   if (t == 0) {
     const int h = (int)(row % Hq);
@@ -363,7 +376,7 @@ hipError_t launch_decode128(const Problem& p, const void* q, const void* k, cons
   hipLaunchKernelGGL(decode128_kernel, dim3((unsigned)(S * p.Hkv * p.B)), dim3(64), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st,
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)rows), dim3(kMergeThreads), 0, st,
                      rows, S, p.Nq, p.Hq, o_part, m_part, l_part, o, m, l);
   return hipGetLastError();
 }
