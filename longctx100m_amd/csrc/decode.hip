@@ -89,10 +89,13 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   ld.init(ks, 0, lane);
   auto issue = [&](int j) {  // V tile j into stage j % kStages
     const int st = j % kStages;
-    ld.load(vbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk, t128::lds_addr(vbuf) + st * kTileBytes, 0, lane);
+    ld.load<false, true>(vbase, ks, (int)(kb0 + (int64_t)j * TK), a.Nk,
+                         t128::lds_addr(vbuf) + st * kTileBytes, 0, lane);
   };
   // K tile j straight into VGPRs (no LDS round trip): lane (c, g) holds key
   // 16 mb + c of the tile, dims 32 kk + 8 g, the A operand of S^T = K Q^T.
+  // The cache is read once per step, so K and V are loaded non-temporally
+  // (5.77 -> 6.58 TB/s per layer against the same kernel with default loads).
   auto kload = [&](int j, bf16x8 (&kr)[2][4]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
@@ -100,7 +103,8 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
       row = row < a.Nk ? row : a.Nk - 1;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
-        kr[mb][kk] = *reinterpret_cast<const bf16x8*>(kbase + row * ks + 32 * kk + 8 * g);
+        kr[mb][kk] = __builtin_nontemporal_load(
+            reinterpret_cast<const bf16x8*>(kbase + row * ks + 32 * kk + 8 * g));
     }
   };
 

@@ -14,6 +14,8 @@
 namespace lc {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kRows = 4;
 constexpr int kUnroll = 4;
 constexpr int kSplit = 4;  // waves per workgroup, each over 1/kSplit of the row
@@ -60,7 +62,11 @@ __global__ __launch_bounds__(64 * kSplit) void gemv_bf16_kernel(int64_t n, int k
       const bool in = c < ce;
       xc[u] = in ? xv[c] : uint4{0, 0, 0, 0};
 #pragma unroll
-      for (int r = 0; r < kRows; ++r) wc[r][u] = in ? wr[r][c] : uint4{0, 0, 0, 0};
+      for (int r = 0; r < kRows; ++r) {  // weights stream once per token: non-temporal
+        const u32x4 v = in ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&wr[r][c]))
+                           : u32x4{0, 0, 0, 0};
+        wc[r][u] = uint4{v[0], v[1], v[2], v[3]};
+      }
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)

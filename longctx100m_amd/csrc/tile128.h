@@ -87,7 +87,14 @@ __device__ __forceinline__ void dma_b128(const void* base, uint32_t off, uint32_
                : "memory");
 }
 
-// Same, non-temporal (streaming data read once: L2 does not keep it).
+// Non-temporal forms (streaming data read once: L2 does not keep it).
+__device__ __forceinline__ void dma_b128_nt(const void* g, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off nt"
+               :
+               : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
 __device__ __forceinline__ void dma_b128_nt(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :
@@ -127,8 +134,9 @@ struct RowLoader {
   // lds: LDS byte address of the tile.  kTracked: issue through the compiler
   // builtin, whose DMA the compiler tracks (it then waits for the DMA before
   // any later LDS read); otherwise through the untracked form above, and the
-  // caller waits.
-  template <bool kTracked = false>
+  // caller waits.  kNt (untracked only): non-temporal loads, for a stream
+  // that no other workgroup reads again.
+  template <bool kTracked = false, bool kNt = false>
   __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int row0, int nrows,
                                        uint32_t lds, int wave, int lane) const {
     if (row0 + ROWS <= nrows) {
@@ -138,6 +146,8 @@ struct RowLoader {
         const uint32_t dst = lds + wave_lds + i * NW * 4 * kRowBytes;
         if constexpr (kTracked)
           __builtin_amdgcn_global_load_lds(tb + off[i], (lds_void*)(uintptr_t)dst, 16, 0, 0);
+        else if constexpr (kNt)
+          dma_b128_nt(tb, off[i], dst);
         else
           dma_b128(tb, off[i], dst);
       }
@@ -152,6 +162,8 @@ struct RowLoader {
         const uint32_t dst = lds + wave_lds + i * NW * 4 * kRowBytes;
         if constexpr (kTracked)
           __builtin_amdgcn_global_load_lds(g, (lds_void*)(uintptr_t)dst, 16, 0, 0);
+        else if constexpr (kNt)
+          dma_b128_nt(g, dst);
         else
           dma_b128(g, dst);
       }
