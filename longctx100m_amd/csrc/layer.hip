@@ -57,6 +57,61 @@ __device__ __forceinline__ void store8<float>(float* p, const f32x8& v) {
   *reinterpret_cast<float4*>(p + 4) = float4{v[4], v[5], v[6], v[7]};
 }
 
+
+// Non-temporal forms, for the prefill's streams: read or written once, far
+// larger than the caches.  (A decode step's single rows are read right after
+// they are written, so they keep the default policy.)
+template <typename T>
+__device__ __forceinline__ f32x8 load8_nt(const T* p);
+template <>
+__device__ __forceinline__ f32x8 load8_nt<uint16_t>(const uint16_t* p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 u = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  f32x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[2 * i] = __uint_as_float(u[i] << 16);
+    r[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+  return r;
+}
+template <>
+__device__ __forceinline__ f32x8 load8_nt<float>(const float* p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 a = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+  const f4 b = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p + 4));
+  return f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+template <typename T>
+__device__ __forceinline__ void store8_nt(T* p, const f32x8& v);
+template <>
+__device__ __forceinline__ void store8_nt<uint16_t>(uint16_t* p, const f32x8& v) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  u4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+  __builtin_nontemporal_store(w, reinterpret_cast<u4*>(p));
+}
+template <>
+__device__ __forceinline__ void store8_nt<float>(float* p, const f32x8& v) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(p));
+  __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(p + 4));
+}
+template <typename T, bool NT>
+__device__ __forceinline__ f32x8 ld8(const T* p) {
+  if constexpr (NT) return load8_nt<T>(p);
+  else return load8<T>(p);
+}
+template <typename T, bool NT>
+__device__ __forceinline__ void st8(T* p, const f32x8& v) {
+  if constexpr (NT) store8_nt<T>(p, v);
+  else store8<T>(p, v);
+}
+// Row counts from which the row kernels stream non-temporally (prefill shapes).
+constexpr int64_t kStreamRows = 1024;
+
 // Round to the storage type and back (identity for fp32).
 template <typename T>
 __device__ __forceinline__ float rnd(float x);
@@ -81,7 +136,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // of squares and the scaling.  Chunk i of lane l in wave w of the row is
 // chunk (64 w + l) + 64 WPR i of the row.  With at most 8 chunks per lane the
 // row, the residual and the weight chunks fit the registers without spilling.
-template <typename T, int NC, int WPR>
+template <typename T, int NC, int WPR, bool NT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, float eps,
                                                       const T* __restrict__ x, int64_t xs,
                                                       const T* __restrict__ res, int64_t rs,
@@ -102,11 +157,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, fl
   // normalises single rows, where that latency is the whole cost).
   f32x8 v[NC];
 #pragma unroll
-  for (int i = 0; i < NC; ++i) v[i] = load8<T>(x + row * xs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
+  for (int i = 0; i < NC; ++i) v[i] = ld8<T, NT>(x + row * xs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
   if (res != nullptr) {
     f32x8 r[NC];
 #pragma unroll
-    for (int i = 0; i < NC; ++i) r[i] = load8<T>(res + row * rs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
+    for (int i = 0; i < NC; ++i) r[i] = ld8<T, NT>(res + row * rs + 8 * min(c0 + 64 * WPR * i, nchunk - 1));
 #pragma unroll
     for (int i = 0; i < NC; ++i)
 #pragma unroll
@@ -115,7 +170,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, fl
 #pragma unroll
       for (int i = 0; i < NC; ++i) {
         const int c = c0 + 64 * WPR * i;
-        if (c < nchunk) store8<T>(res_out + row * ros + 8 * c, v[i]);
+        if (c < nchunk) st8<T, NT>(res_out + row * ros + 8 * c, v[i]);
       }
     }
   }
@@ -147,7 +202,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int cols, fl
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = c0 + 64 * WPR * i;
-    if (c < nchunk) store8<T>(out + row * os + 8 * c, v[i]);
+    if (c < nchunk) st8<T, NT>(out + row * os + 8 * c, v[i]);
   }
 }
 
@@ -162,12 +217,13 @@ hipError_t launch_rmsnorm_t(int64_t rows, int cols, float eps, const void* x, in
                        static_cast<const T*>(res), rs, static_cast<T*>(res_out), ros,
                        static_cast<const T*>(w), static_cast<T*>(out), os);
   };
+  const bool nt = rows >= kStreamRows;
   if (nchunk <= 64 * 2)
-    args(rmsnorm_kernel<T, 2, 1>, 4);
+    nt ? args(rmsnorm_kernel<T, 2, 1, true>, 4) : args(rmsnorm_kernel<T, 2, 1, false>, 4);
   else if (nchunk <= 64 * 8)
-    args(rmsnorm_kernel<T, 8, 1>, 4);
+    nt ? args(rmsnorm_kernel<T, 8, 1, true>, 4) : args(rmsnorm_kernel<T, 8, 1, false>, 4);
   else  // up to 64 * 4 * 8 chunks = 16384 columns
-    args(rmsnorm_kernel<T, 8, 4>, 1);
+    nt ? args(rmsnorm_kernel<T, 8, 4, true>, 1) : args(rmsnorm_kernel<T, 8, 4, false>, 1);
   return hipGetLastError();
 }
 
@@ -199,7 +255,7 @@ __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableArgs a) {
 
 // One thread per (token, head, 8 rotation pairs): x1 = x[8c..8c+7] and
 // x2 = x[half+8c..], out1 = x1*cos - x2*sin, out2 = x2*cos + x1*sin.
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(256) void rope_apply_kernel(int64_t tokens, int heads, int half,
                                                          const float* table, const T* src,
                                                          int64_t sts, T* dst) {
@@ -213,8 +269,8 @@ __global__ __launch_bounds__(256) void rope_apply_kernel(int64_t tokens, int hea
   const int64_t t = th / heads;
   const T* s = src + t * sts + (int64_t)h * 2 * half + 8 * c;
   T* d = dst + (t * heads + h) * 2 * half + 8 * c;
-  const f32x8 x1 = load8<T>(s);
-  const f32x8 x2 = load8<T>(s + half);
+  const f32x8 x1 = ld8<T, NT>(s);
+  const f32x8 x2 = ld8<T, NT>(s + half);
   const float* tr = table + t * 2 * half + 8 * c;
   const f32x8 cs = load8<float>(tr);
   const f32x8 sn = load8<float>(tr + half);
@@ -224,12 +280,12 @@ __global__ __launch_bounds__(256) void rope_apply_kernel(int64_t tokens, int hea
     o1[j] = x1[j] * cs[j] - x2[j] * sn[j];
     o2[j] = x2[j] * cs[j] + x1[j] * sn[j];
   }
-  store8<T>(d, o1);
-  store8<T>(d + half, o2);
+  st8<T, NT>(d, o1);
+  st8<T, NT>(d + half, o2);
 }
 
 // ----------------------------------------------------------------- SwiGLU --
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(256) void swiglu_kernel(int64_t rows, int cols, const T* g,
                                                      int64_t gs, const T* u, int64_t us,
                                                      T* out) {
@@ -238,15 +294,15 @@ __global__ __launch_bounds__(256) void swiglu_kernel(int64_t rows, int cols, con
   if (idx >= rows * cpr) return;
   const int64_t r = idx / cpr;
   const int c = (int)(idx - r * cpr);
-  const f32x8 gv = load8<T>(g + r * gs + 8 * c);
-  const f32x8 uv = load8<T>(u + r * us + 8 * c);
+  const f32x8 gv = ld8<T, NT>(g + r * gs + 8 * c);
+  const f32x8 uv = ld8<T, NT>(u + r * us + 8 * c);
   f32x8 o;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float sl = rnd<T>(__fdiv_rn(gv[j], __fadd_rn(1.0f, expf(-gv[j]))));
     o[j] = __fmul_rn(sl, uv[j]);
   }
-  store8<T>(out + r * (int64_t)cols + 8 * c, o);
+  st8<T, NT>(out + r * (int64_t)cols + 8 * c, o);
 }
 
 unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -286,14 +342,20 @@ hipError_t launch_rope_apply(int dtype, int64_t tokens, int heads, int head_dim,
   const int half = head_dim / 2;
   const int64_t n = tokens * heads * (half / 8);
   if (n <= 0) return hipSuccess;
-  if (dtype == 1)
-    hipLaunchKernelGGL(rope_apply_kernel<uint16_t>, dim3(blocks_for(n)), dim3(256), 0, s, tokens,
-                       heads, half, table, static_cast<const uint16_t*>(src), sts,
-                       static_cast<uint16_t*>(dst));
-  else
-    hipLaunchKernelGGL(rope_apply_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, tokens,
-                       heads, half, table, static_cast<const float*>(src), sts,
-                       static_cast<float*>(dst));
+  auto go = [&](auto kernel, auto* src_t, auto* dst_t) {
+    hipLaunchKernelGGL(kernel, dim3(blocks_for(n)), dim3(256), 0, s, tokens, heads, half, table,
+                       src_t, sts, dst_t);
+  };
+  const bool nt = tokens >= kStreamRows;
+  if (dtype == 1) {
+    const uint16_t* sp = static_cast<const uint16_t*>(src);
+    uint16_t* dp = static_cast<uint16_t*>(dst);
+    nt ? go(rope_apply_kernel<uint16_t, true>, sp, dp) : go(rope_apply_kernel<uint16_t, false>, sp, dp);
+  } else {
+    const float* sp = static_cast<const float*>(src);
+    float* dp = static_cast<float*>(dst);
+    nt ? go(rope_apply_kernel<float, true>, sp, dp) : go(rope_apply_kernel<float, false>, sp, dp);
+  }
   return hipGetLastError();
 }
 
@@ -301,14 +363,22 @@ hipError_t launch_swiglu(int dtype, int64_t rows, int cols, const void* g, int64
                          const void* u, int64_t us, void* out, hipStream_t s) {
   const int64_t n = rows * (cols / 8);
   if (n <= 0) return hipSuccess;
-  if (dtype == 1)
-    hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3(blocks_for(n)), dim3(256), 0, s, rows, cols,
-                       static_cast<const uint16_t*>(g), gs, static_cast<const uint16_t*>(u), us,
-                       static_cast<uint16_t*>(out));
-  else
-    hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s, rows, cols,
-                       static_cast<const float*>(g), gs, static_cast<const float*>(u), us,
-                       static_cast<float*>(out));
+  auto go = [&](auto kernel, auto* g_t, auto* u_t, auto* o_t) {
+    hipLaunchKernelGGL(kernel, dim3(blocks_for(n)), dim3(256), 0, s, rows, cols, g_t, gs, u_t, us,
+                       o_t);
+  };
+  const bool nt = rows >= kStreamRows;
+  if (dtype == 1) {
+    const uint16_t* gp = static_cast<const uint16_t*>(g);
+    const uint16_t* up = static_cast<const uint16_t*>(u);
+    uint16_t* op = static_cast<uint16_t*>(out);
+    nt ? go(swiglu_kernel<uint16_t, true>, gp, up, op) : go(swiglu_kernel<uint16_t, false>, gp, up, op);
+  } else {
+    const float* gp = static_cast<const float*>(g);
+    const float* up = static_cast<const float*>(u);
+    float* op = static_cast<float*>(out);
+    nt ? go(swiglu_kernel<float, true>, gp, up, op) : go(swiglu_kernel<float, false>, gp, up, op);
+  }
   return hipGetLastError();
 }
 

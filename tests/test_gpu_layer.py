@@ -103,10 +103,11 @@ def test_rope_table(ly, gpu, scaling):
     np.testing.assert_allclose(tab, want, rtol=0, atol=4e-7)
 
 
+@pytest.mark.parametrize("T", [96, 1100])  # 1100 tokens: the non-temporal (prefill) kernel
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_rope_apply_strided_and_in_place(ly, gpu, dtype):
+def test_rope_apply_strided_and_in_place(ly, gpu, dtype, T):
     rng = np.random.default_rng(5)
-    T, hq, hkv, d = 96, 6, 2, 128
+    hq, hkv, d = 6, 2, 128
     tdt = _dt(gpu, dtype)
     qkv = rng.standard_normal((T, (hq + 2 * hkv) * d)).astype(np.float32)
     if dtype == "bf16":
@@ -125,10 +126,11 @@ def test_rope_apply_strided_and_in_place(ly, gpu, dtype):
     np.testing.assert_array_equal(_np(kc).reshape(T, hkv, d), _np(k))
 
 
+@pytest.mark.parametrize("rows", [33, 1100])  # 1100 rows: the non-temporal (prefill) kernel
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_swiglu(ly, gpu, dtype):
+def test_swiglu(ly, gpu, dtype, rows):
     rng = np.random.default_rng(6)
-    rows, inter = 33, 2048
+    inter = 2048
     gu = (rng.standard_normal((rows, 2 * inter)) * 4).astype(np.float32)
     gu[0, :4] = [-120.0, 120.0, 0.0, -0.0]
     if dtype == "bf16":
