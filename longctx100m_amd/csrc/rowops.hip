@@ -147,10 +147,10 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(int64_t rows, int N
     for (int c = sub; c < nc; c += 16) {
       u32x4 ov[kPer], gv[kPer];
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {  // every load of the pass issued before use
+      for (int i = 0; i < kPer; ++i) {  // every load of the pass issued before use; read once
         const int64_t off = min(r0 + 16 * i, rows - 1) * D + (int64_t)c * VEC;
-        ov[i] = *reinterpret_cast<const u32x4*>(out + off);
-        gv[i] = *reinterpret_cast<const u32x4*>(dout + off);
+        ov[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(out + off));
+        gv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dout + off));
       }
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
