@@ -22,6 +22,12 @@ the backward is 2.5x the forward.  Peak: bf16 dense MFMA 2516.6 TFLOP/s.
 The CPU baseline times the C restatement of the reference algorithm
 (oracle/ring_ref.c, OpenMP on the host cores) on a bounded sample: one head
 of the same geometry with a shorter shard, sized to ~15 s.
+
+After the headline measurement, with its tensors freed, the default run also
+measures the other configurations that fit one GPU in short runs (config 5's
+1M-token forward, the C4 prefill attention share, the C4 decode step) and
+adds their summaries to the same line under "other_configs";
+--no-other-configs skips them.
 """
 
 from __future__ import annotations
@@ -79,6 +85,9 @@ def parse():
                     help="forward with each later hop into its own partial buffers and the "
                          "lc_attn_merge kernel per hop, instead of the merge in the forward's "
                          "epilogue (measures the merge kernel's HBM rate in the step)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the short runs of configs 5, 4 (prefill attention) and the C4 decode "
+                         "that follow the headline measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -220,7 +229,7 @@ def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
     return sum(per[k] for k in names)
 
 
-def long_shard(args, torch, ra) -> int:
+def long_shard_line(torch, ra, steps: int, warmup: int) -> dict:
     """rank 1 of a 2-shard layout with 1,000,000 local tokens,
     Hq = Hkv = 16, d = 128, bf16; forward over the diagonal block and one full
     incoming shard, merged by LSE (1M mod 128 = 64, so every kernel runs tail tiles)."""
@@ -243,8 +252,7 @@ def long_shard(args, torch, ra) -> int:
     def step():
         lsf.forward()
 
-    steps = max(1, min(args.steps, 2))
-    for _ in range(max(0, min(args.warmup, 1))):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     log("long shard: warmup done")
@@ -270,6 +278,11 @@ def long_shard(args, torch, ra) -> int:
         "hbm_footprint_gb": {"resident_tensors": round(resident / 1e9, 3),
                              "torch_peak_allocated": round(torch.cuda.max_memory_allocated() / 1e9, 3)},
     }
+    return line
+
+
+def long_shard(args, torch, ra) -> int:
+    line = long_shard_line(torch, ra, max(1, min(args.steps, 2)), max(0, min(args.warmup, 1)))
     print(json.dumps(line), flush=True)
     return 0
 
@@ -362,7 +375,7 @@ def host_path(args, torch, ra) -> int:
     return 0
 
 
-def c4_prefill(args, torch, ra) -> int:
+def c4_prefill_line(torch, ra, steps: int, warmup: int) -> dict:
     """The C4 model's attention share on one GPU (prefill): GQA Hq=32 / Hkv=8,
     d=128, bf16, 65,536 local tokens at rank 3 of a 4-rank ring, i.e. the
     diagonal block plus 3 preceding 65,536-token KV shards, merged by LSE.
@@ -381,8 +394,7 @@ def c4_prefill(args, torch, ra) -> int:
     def step():
         return ra.ring_causal_attention_forward_with_stats(shards, rank)
 
-    steps = max(1, min(args.steps, 3))
-    for _ in range(max(0, min(args.warmup, 1))):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     log("C4 prefill attention: warmup done")
@@ -408,6 +420,11 @@ def c4_prefill(args, torch, ra) -> int:
         "model_attention_ms_24_layers": round(24 * ms, 1),
         "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3),
     }
+    return line
+
+
+def c4_prefill(args, torch, ra) -> int:
+    line = c4_prefill_line(torch, ra, max(1, min(args.steps, 3)), max(0, min(args.warmup, 1)))
     print(json.dumps(line), flush=True)
     return 0
 
@@ -498,7 +515,7 @@ def c4_model(args, torch, ra) -> int:
     return 0
 
 
-def c4_decode(args, torch, ra) -> int:
+def c4_decode_line(torch, ra, steps: int, warmup: int) -> dict:
     """Incremental decode of the C4 model on one GPU: one new token against a
     KV cache of 262,144 tokens per layer (the 4 x 65,536-token context of
     config 4), through embedding, 24 layers (GEMVs, RoPE, split-KV decode
@@ -510,7 +527,6 @@ def c4_decode(args, torch, ra) -> int:
 
     cfg = ly.C4
     ctx, d, hkv = 4 * 65536, cfg.head_dim, cfg.num_key_value_heads
-    steps = max(1, args.steps)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
@@ -518,7 +534,7 @@ def c4_decode(args, torch, ra) -> int:
     torch.cuda.reset_peak_memory_stats()
     log(f"C4 decode: {cfg.num_layers} layers, KV cache of {ctx} tokens per layer")
     weights = ly.init_model_weights(cfg, gen, dev)
-    cap = ctx + steps + max(0, args.warmup) + 1
+    cap = ctx + steps + warmup + 1
     caches = []
     for _ in range(cfg.num_layers):
         caches.append(tuple(torch.randn(1, cap, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
@@ -531,7 +547,7 @@ def c4_decode(args, torch, ra) -> int:
                      dtype=torch.uint8, device=dev)
     log("C4 decode: weights and caches ready")
     pos = ctx
-    for _ in range(max(0, args.warmup)):
+    for _ in range(warmup):
         ly.model_decode_step(7, pos, weights, cfg, table, caches, ws)
         pos += 1
     torch.cuda.synchronize()
@@ -580,8 +596,39 @@ def c4_decode(args, torch, ra) -> int:
         "logits_shape": list(logits.shape),
         "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
     }
+    return line
+
+
+def c4_decode(args, torch, ra) -> int:
+    line = c4_decode_line(torch, ra, max(1, args.steps), max(0, args.warmup))
     print(json.dumps(line), flush=True)
     return 0
+
+
+# Measured after the headline line's timed region (and its CPU baseline) with
+# its tensors freed: name -> (measuring function, timed steps, warmup steps).
+OTHER_CONFIGS = {
+    "c5_long_shard_fwd": (long_shard_line, 1, 1),
+    "c4_prefill_attention": (c4_prefill_line, 2, 1),
+    "c4_decode": (c4_decode_line, 5, 2),
+}
+SUMMARY_KEYS = ("metric", "value", "unit", "higher_is_better", "steps", "ms_per_step",
+                "pct_mfma_peak", "roofline", "config")
+
+
+def other_configs(torch, ra) -> dict:
+    """The other BASELINE configurations that fit one GPU, each a short run:
+    the summary of the line its own flag prints (the full line comes from
+    bench.py --long-shard / --c4-prefill / --c4-decode)."""
+    out = {}
+    for name, (fn, steps, warmup) in OTHER_CONFIGS.items():
+        t0 = time.perf_counter()
+        line = fn(torch, ra, steps, warmup)
+        torch.cuda.empty_cache()
+        out[name] = {k: line[k] for k in SUMMARY_KEYS if k in line}
+        out[name]["wall_s"] = round(time.perf_counter() - t0, 1)
+        log(f"{name}: {line['value']} {line['unit']} ({out[name]['wall_s']} s)")
+    return out
 
 
 def main() -> int:
@@ -633,6 +680,7 @@ def main() -> int:
                   separate_merge=args.separate_merge)
     owners = rs.owners
     ws = rs.workspace
+    shares_ds = ws is not None
     if ws is not None:
         log(f"dS exchange workspace: {ws.numel() / 2**30:.1f} GiB")
 
@@ -716,6 +764,10 @@ def main() -> int:
                     if sclk and sclk["mean"] > 0 else None),
                 "box": socket.gethostname()}
 
+    del rs, q, dout, ks, vs, ws
+    torch.cuda.empty_cache()
+    others = None if args.no_other_configs else other_configs(torch, ra)
+
     cpu = None
     if args.cpu_seconds > 0:
         log("cpu baseline (C restatement of the reference algorithm) ...")
@@ -744,7 +796,7 @@ def main() -> int:
                          f"shard, Hq=Hkv={h}, d={d}; fwd over diagonal + {n_full} full KV shards "
                          f"with LSE merge" + (" (merge kernel per hop)" if args.separate_merge
                                               else "") + ", then recompute bwd (dQ across shards, dK/dV per "
-                         f"shard; " + ("dS shared by the dK/dV and dQ kernels)" if ws is not None
+                         f"shard; " + ("dS shared by the dK/dV and dQ kernels)" if shares_ds
                                        else "dQ kernel recomputes dS)")),
             "world": world, "rank": rank, "local_tokens": n, "heads_q": h, "heads_kv": h,
             "head_dim": d, "parallelism": "one rank's share on one GPU (ring emulated in HBM)",
@@ -754,6 +806,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kern,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
     return 0
