@@ -91,6 +91,65 @@ int lc_swiglu(int32_t dtype, int64_t rows, int32_t cols, const void* gate, int64
 int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_stride,
             const void* x, void* y, void* stream);
 
+/* lc_gemv with the row operation before it or after it folded in, so that one
+ * launch does what the decode step of a decoder layer otherwise spreads over
+ * a norm, a projection and a RoPE / SwiGLU / cast launch.  Every result is
+ * bit-identical to the unfused sequence of this library's entry points (same
+ * fp32 operations, same reduction orders, bf16 rounding at the same points).
+ * The composed reference ops: RmsNorm::forward (model.rs:53-62) with the
+ * decoder's residual add (:387-393), the attention output cast to the model
+ * dtype, Linear (:64-76), rotate-half RoPE of q and k (rope.rs:116-127) with
+ * the token's k and v appended to the KV cache, and SwiGLU (:323-327).
+ *
+ * Input forms (the bf16 vector the projection multiplies):
+ *   LC_GEMV_IN_BF16     x is bf16 [cols], as lc_gemv;
+ *   LC_GEMV_IN_F32      x is fp32 [cols], rounded to bf16 (nearest even) first;
+ *   LC_GEMV_IN_RMSNORM  x is bf16 [cols]; the vector is lc_rmsnorm of the one
+ *                       row x (+ residual) with norm_weight and eps, and
+ *                       x + residual is written to residual_out when that is
+ *                       set (cols <= 4096).
+ * Output forms:
+ *   LC_GEMV_OUT_PLAIN     y [rows], as lc_gemv;
+ *   LC_GEMV_OUT_SWIGLU    rows = 2 I (gate rows, then up rows, as one fused
+ *                         gate/up weight): y [I] = lc_swiglu(gate, up) of the
+ *                         two bf16 halves of the product;
+ *   LC_GEMV_OUT_ROPE_QKV  rows = (q_heads + 2 kv_heads) head_dim (one fused
+ *                         q/k/v weight): y [q_heads head_dim] = lc_rope_apply
+ *                         of the q part, k_out [kv_heads head_dim] = that of
+ *                         the k part, v_out [kv_heads head_dim] = the v part;
+ *                         rope_row is one token's row of lc_rope_table
+ *                         ([2, head_dim / 2] fp32), head_dim a multiple of 16
+ *                         and <= 256 (as lc_rope_apply).  k_out and v_out may be the token's rows
+ *                         of a KV cache.
+ * bf16 weights only; cols and w_stride multiples of 8, w_stride >= cols; w,
+ * x, residual, residual_out and norm_weight 16-byte aligned. */
+#define LC_GEMV_IN_BF16 0
+#define LC_GEMV_IN_F32 1
+#define LC_GEMV_IN_RMSNORM 2
+#define LC_GEMV_OUT_PLAIN 0
+#define LC_GEMV_OUT_SWIGLU 1
+#define LC_GEMV_OUT_ROPE_QKV 2
+
+typedef struct lc_gemv_fused {
+  int32_t in_form;
+  int32_t out_form;
+  /* LC_GEMV_IN_RMSNORM */
+  const void* residual;    /* bf16 [cols] or NULL */
+  void* residual_out;      /* bf16 [cols] or NULL (needs residual) */
+  const void* norm_weight; /* bf16 [cols] */
+  float eps;
+  /* LC_GEMV_OUT_ROPE_QKV */
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  const float* rope_row;
+  void* k_out; /* bf16 [kv_heads * head_dim] */
+  void* v_out; /* bf16 [kv_heads * head_dim] */
+} lc_gemv_fused_t;
+
+int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const void* w,
+                  int64_t w_stride, const void* x, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,27 @@ class Rope(ctypes.Structure):
     ]
 
 
+LC_GEMV_IN_BF16, LC_GEMV_IN_F32, LC_GEMV_IN_RMSNORM = 0, 1, 2
+LC_GEMV_OUT_PLAIN, LC_GEMV_OUT_SWIGLU, LC_GEMV_OUT_ROPE_QKV = 0, 1, 2
+
+
+class GemvFused(ctypes.Structure):
+    _fields_ = [
+        ("in_form", c_int32),
+        ("out_form", c_int32),
+        ("residual", c_void_p),
+        ("residual_out", c_void_p),
+        ("norm_weight", c_void_p),
+        ("eps", ctypes.c_float),
+        ("q_heads", c_int32),
+        ("kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("rope_row", c_void_p),
+        ("k_out", c_void_p),
+        ("v_out", c_void_p),
+    ]
+
+
 _vpp = POINTER(c_void_p)
 _S, _M, _R = POINTER(Shape), POINTER(Mask), POINTER(RingDesc)
 
@@ -129,6 +150,8 @@ SIGNATURES = {
                           c_void_p, c_void_p]),
     "lc_gemv": (c_int, [c_int32, c_int64, c_int32, c_void_p, c_int64, c_void_p, c_void_p,
                         c_void_p]),
+    "lc_gemv_fused": (c_int, [POINTER(GemvFused), c_int64, c_int32, c_void_p, c_int64, c_void_p,
+                              c_void_p, c_void_p]),
     "lc_last_error": (ctypes.c_char_p, []),
     "lc_abi_version": (c_int32, []),
 }

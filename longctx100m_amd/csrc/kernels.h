@@ -122,6 +122,11 @@ hipError_t launch_rope_apply(int dtype, int64_t tokens, int heads, int head_dim,
 // ws elements), bf16 x [k]; k % 8 == 0, ws % 8 == 0, 16-byte aligned (gemv.hip).
 hipError_t launch_gemv_bf16(int64_t n, int k, const void* w, int64_t ws, const void* x, void* y,
                             hipStream_t s);
+// lc_gemv_fused's launch (forms as LC_GEMV_IN_* / LC_GEMV_OUT_*).
+hipError_t launch_gemv_fused(int in_form, int out_form, int64_t rows, int cols, const void* w,
+                             int64_t ws, const void* x, void* y, const void* res, void* res_out,
+                             const void* nw, float eps, int q_heads, int kv_heads, int head_dim,
+                             const float* rope, void* k_out, void* v_out, hipStream_t s);
 hipError_t launch_swiglu(int dtype, int64_t rows, int cols, const void* g, int64_t gs,
                          const void* u, int64_t us, void* out, hipStream_t s);
 

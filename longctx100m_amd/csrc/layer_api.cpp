@@ -174,4 +174,59 @@ int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_
   return e == hipSuccess ? LC_OK : hip_error(e, "gemv launch");
 }
 
+int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const void* w,
+                  int64_t w_stride, const void* x, void* y, void* stream) {
+  if (!f) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (rows < 0 || cols <= 0 || cols % 8 != 0)
+    return set_error(LC_ERR_INVALID, "gemv needs rows >= 0 and cols > 0, cols %% 8 == 0");
+  if (!w || !x || !y) return set_error(LC_ERR_INVALID, "null pointer argument");
+  if (!stride_ok(w_stride, cols))
+    return set_error(LC_ERR_INVALID, "row strides must be >= cols and multiples of 8 elements");
+  if (!aligned16(w) || !aligned16(x))
+    return set_error(LC_ERR_INVALID, "gemv w and x must be 16-byte aligned");
+  switch (f->in_form) {
+    case LC_GEMV_IN_BF16:
+    case LC_GEMV_IN_F32:
+      break;
+    case LC_GEMV_IN_RMSNORM:
+      if (cols > 4096)
+        return set_error(LC_ERR_INVALID, "the folded rmsnorm needs cols <= 4096");
+      if (!f->norm_weight) return set_error(LC_ERR_INVALID, "rmsnorm needs norm_weight");
+      if (f->residual_out && !f->residual)
+        return set_error(LC_ERR_INVALID, "residual_out needs a residual input");
+      if (!aligned16(f->norm_weight) || (f->residual && !aligned16(f->residual)) ||
+          (f->residual_out && !aligned16(f->residual_out)))
+        return set_error(LC_ERR_INVALID, "rmsnorm pointers must be 16-byte aligned");
+      if (!(f->eps >= 0.f)) return set_error(LC_ERR_INVALID, "eps must be non-negative");
+      break;
+    default:
+      return set_error(LC_ERR_INVALID, "unknown gemv input form %d", f->in_form);
+  }
+  switch (f->out_form) {
+    case LC_GEMV_OUT_PLAIN:
+      break;
+    case LC_GEMV_OUT_SWIGLU:
+      if (rows % 4 != 0)
+        return set_error(LC_ERR_INVALID, "the swiglu form needs rows (2 x intermediate) %% 4 == 0");
+      break;
+    case LC_GEMV_OUT_ROPE_QKV:
+      if (f->q_heads <= 0 || f->kv_heads <= 0 || f->head_dim <= 0 || f->head_dim % 16 != 0 ||
+          f->head_dim > 256)
+        return set_error(LC_ERR_INVALID, "rope form needs heads > 0 and head_dim %% 16 == 0, <= 256");
+      if (rows != (int64_t)(f->q_heads + 2 * (int64_t)f->kv_heads) * f->head_dim)
+        return set_error(LC_ERR_INVALID, "rope form needs rows = (q_heads + 2 kv_heads) head_dim");
+      if (!f->rope_row || !f->k_out || !f->v_out)
+        return set_error(LC_ERR_INVALID, "rope form needs rope_row, k_out and v_out");
+      break;
+    default:
+      return set_error(LC_ERR_INVALID, "unknown gemv output form %d", f->out_form);
+  }
+  if (rows == 0) return LC_OK;
+  hipError_t e = lc::launch_gemv_fused(
+      f->in_form, f->out_form, rows, cols, w, w_stride, x, y, f->residual, f->residual_out,
+      f->norm_weight, f->eps, f->q_heads, f->kv_heads, f->head_dim, f->rope_row, f->k_out,
+      f->v_out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LC_OK : hip_error(e, "gemv launch");
+}
+
 }  // extern "C"

@@ -171,6 +171,76 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x, w.t())
 
 
+def gemv_fused(x: torch.Tensor, w: torch.Tensor, *, norm_weight: Optional[torch.Tensor] = None,
+               eps: float = 0.0, residual: Optional[torch.Tensor] = None,
+               residual_out: Optional[torch.Tensor] = None, swiglu: bool = False,
+               rope_row: Optional[torch.Tensor] = None, heads: Optional[Tuple[int, int]] = None,
+               k_out: Optional[torch.Tensor] = None,
+               v_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One token through lc_gemv_fused: the projection x @ w.T of the decode
+    step with its neighbouring row operation folded in, bit-identical to the
+    unfused calls.
+    * x: bf16 [1, cols], or fp32 [1, cols] (rounded to bf16 first: the
+      attention output cast);
+    * norm_weight (+ eps, residual, residual_out): the multiplied vector is
+      rmsnorm(x (+ residual)) as :func:`rmsnorm` computes it (bf16 x);
+    * swiglu: w holds gate rows then up rows; returns swiglu(gate, up) [1, rows/2];
+    * rope_row (+ heads = (q_heads, kv_heads), k_out, v_out): w is a fused
+      q/k/v weight; returns RoPE(q) [1, q_heads * head_dim] and writes RoPE(k)
+      to k_out and v to v_out (e.g. a KV cache's row of the token)."""
+    _chk_cuda(x, w)
+    rows, cols = w.shape
+    if x.dim() != 2 or x.shape != (1, cols) or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous [1, {cols}] tensor")
+    if w.dtype != torch.bfloat16 or w.stride(1) != 1:
+        raise ValueError("w must be bf16 with contiguous rows")
+    f = _lib.GemvFused()
+    if x.dtype == torch.float32:
+        f.in_form = _lib.LC_GEMV_IN_F32
+    elif x.dtype == torch.bfloat16:
+        f.in_form = _lib.LC_GEMV_IN_BF16
+    else:
+        raise ValueError("x must be bf16 or fp32")
+    if norm_weight is not None:
+        if x.dtype != torch.bfloat16:
+            raise ValueError("the folded rmsnorm takes a bf16 x")
+        _chk_out(norm_weight.view(1, -1), 1, cols, x.dtype, "norm_weight")
+        _chk_out(residual, 1, cols, x.dtype, "residual")
+        _chk_out(residual_out, 1, cols, x.dtype, "residual_out")
+        f.in_form = _lib.LC_GEMV_IN_RMSNORM
+        f.norm_weight = norm_weight.data_ptr()
+        f.eps = float(eps)
+        f.residual = residual.data_ptr() if residual is not None else None
+        f.residual_out = residual_out.data_ptr() if residual_out is not None else None
+    elif residual is not None or residual_out is not None:
+        raise ValueError("residual and residual_out belong to the folded rmsnorm (norm_weight)")
+    if swiglu and rope_row is not None:
+        raise ValueError("one output form: swiglu or rope")
+    if swiglu:
+        f.out_form = _lib.LC_GEMV_OUT_SWIGLU
+        y = torch.empty((1, rows // 2), dtype=torch.bfloat16, device=x.device)
+    elif rope_row is not None:
+        if heads is None or k_out is None or v_out is None:
+            raise ValueError("the rope form needs heads, k_out and v_out")
+        hq, hkv = heads
+        d = rows // (hq + 2 * hkv)
+        if rope_row.dtype != torch.float32 or not rope_row.is_contiguous() or \
+                rope_row.numel() != d or rope_row.device != x.device:
+            raise ValueError(f"rope_row must be one contiguous [2, {d // 2}] fp32 table row")
+        _chk_out(k_out.reshape(1, -1), 1, hkv * d, torch.bfloat16, "k_out")
+        _chk_out(v_out.reshape(1, -1), 1, hkv * d, torch.bfloat16, "v_out")
+        f.out_form = _lib.LC_GEMV_OUT_ROPE_QKV
+        f.q_heads, f.kv_heads, f.head_dim = hq, hkv, d
+        f.rope_row, f.k_out, f.v_out = rope_row.data_ptr(), k_out.data_ptr(), v_out.data_ptr()
+        y = torch.empty((1, hq * d), dtype=torch.bfloat16, device=x.device)
+    else:
+        f.out_form = _lib.LC_GEMV_OUT_PLAIN
+        y = torch.empty((1, rows), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().lc_gemv_fused(ctypes.byref(f), rows, cols, w.data_ptr(), w.stride(0),
+                                         x.data_ptr(), y.data_ptr(), _stream()))
+    return y
+
+
 # ------------------------------------------------------------- the model --
 
 @dataclass
@@ -290,15 +360,33 @@ def layer_flops(cfg: ModelConfig, tokens: int, rank: int) -> Dict[str, float]:
 def layer_decode(x: torch.Tensor, w: Dict[str, torch.Tensor], cfg: ModelConfig,
                  table: torch.Tensor, pos: int, cache: Tuple[torch.Tensor, torch.Tensor],
                  residual: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None):
+                 workspace: Optional[torch.Tensor] = None, fused: bool = True):
     """One decoder layer for the token at position ``pos`` (x [1, hidden]),
     attending to the cache rows 0..pos after appending its own K and V.  The
     reference recomputes the whole prefill for each new token
     (src/longctx100m/distributed_infer.py:185-219,
     rust/longctx100m-model/src/bin/infer.rs:96-106); this computes the same
     last-position result from the cache.  ``table`` row ``pos`` holds the
-    token's RoPE angles.  Returns (x_after_attention, mlp_out) as layer_prefill."""
+    token's RoPE angles.  Returns (x_after_attention, mlp_out) as layer_prefill.
+
+    ``fused`` runs each projection as one lc_gemv_fused launch with its row
+    operation folded in (norm + QKV + RoPE + cache append, the fp32 attention
+    output's cast + o, norm + gate/up + SwiGLU, down): five launches with the
+    attention instead of thirteen, with bit-identical results."""
     d, hq, hkv = cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    if fused:
+        kc, vc = cache
+        xin = torch.empty_like(x) if residual is not None else x
+        q = gemv_fused(x, w["wqkv"], norm_weight=w["norm1"], eps=cfg.rms_norm_eps,
+                       residual=residual, residual_out=xin if residual is not None else None,
+                       rope_row=table[pos], heads=(hq, hkv), k_out=kc[0, pos], v_out=vc[0, pos])
+        o, _, _ = ra.decode(q.view(1, 1, hq, d), kc[:, :pos + 1], vc[:, :pos + 1], q_pos0=pos,
+                            k_pos0=0, workspace=workspace)
+        ao = gemv_fused(o.view(1, hq * d), w["wo"])
+        x2 = torch.empty_like(x)
+        a = gemv_fused(xin, w["wgu"], norm_weight=w["norm2"], eps=cfg.rms_norm_eps, residual=ao,
+                       residual_out=x2, swiglu=True)
+        return x2, gemv_fused(a, w["wd"])
     if residual is not None:
         xin = torch.empty_like(x)
         h = rmsnorm(x, w["norm1"], cfg.rms_norm_eps, residual=residual, residual_out=xin)
@@ -344,14 +432,19 @@ def model_prefill(ids: torch.Tensor, weights: Dict, cfg: ModelConfig, table: tor
 
 
 def model_decode_step(token: int, pos: int, weights: Dict, cfg: ModelConfig,
-                      table: torch.Tensor, caches, workspace=None) -> torch.Tensor:
-    """Logits [1, vocab] of the token at ``pos`` given caches holding 0..pos-1."""
+                      table: torch.Tensor, caches, workspace=None,
+                      fused: bool = True) -> torch.Tensor:
+    """Logits [1, vocab] of the token at ``pos`` given caches holding 0..pos-1
+    (``fused`` as layer_decode)."""
     dev = weights["embed"].device
     x = torch.nn.functional.embedding(torch.tensor([token], device=dev), weights["embed"])
     res = None
     for li, lw in enumerate(weights["layers"]):
         x, res = layer_decode(x, lw, cfg, table, pos, caches[li], residual=res,
-                              workspace=workspace)
+                              workspace=workspace, fused=fused)
+    # The final norm stays a launch of its own: folded into the LM head
+    # (32,064 row blocks) its per-workgroup cost outweighs the launch it saves
+    # (155-161 us against 151 us).
     h = rmsnorm(x, weights["final_norm"], cfg.rms_norm_eps, residual=res)
     return linear(h, weights["lm_head"])
 

@@ -43,6 +43,8 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.RingDesc) == 64
     assert ctypes.sizeof(_lib.Rope) == 56
     assert _lib.RingDesc.valid_length.offset == 48
+    assert ctypes.sizeof(_lib.GemvFused) == 72
+    assert _lib.GemvFused.eps.offset == 32 and _lib.GemvFused.rope_row.offset == 48
 
 
 def _desc(**kw):
@@ -184,6 +186,38 @@ def test_gemv_argument_errors(lib):
     assert lib.lc_gemv(bf, 4, 8, 24, 8, 16, 16, None) == _lib.LC_ERR_INVALID
     assert "aligned" in lib.lc_last_error().decode()
     assert lib.lc_gemv(bf, 0, 8, 16, 8, 16, 16, None) == _lib.LC_OK
+
+
+def test_gemv_fused_argument_errors(lib):
+    """lc_gemv_fused checks its forms before any launch.  Every call here fails
+    a check or has rows = 0 (which returns after the checks), so none reaches
+    a launch with these placeholder pointers."""
+    G = _lib.GemvFused
+
+    def call(f, rows=0, cols=64):
+        rc = lib.lc_gemv_fused(ctypes.byref(f) if f is not None else None, rows, cols, 16, cols,
+                               16, 16, None)
+        return rc, lib.lc_last_error().decode()
+
+    assert call(None)[0] == _lib.LC_ERR_INVALID
+    assert call(G(in_form=3)) == (_lib.LC_ERR_INVALID, "unknown gemv input form 3")
+    assert call(G(out_form=5)) == (_lib.LC_ERR_INVALID, "unknown gemv output form 5")
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16), cols=4104)[1] == \
+        "the folded rmsnorm needs cols <= 4096"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM))[1] == "rmsnorm needs norm_weight"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, residual_out=16))[1] == \
+        "residual_out needs a residual input"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=24))[1] == \
+        "rmsnorm pointers must be 16-byte aligned"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, eps=-1.0))[1] == \
+        "eps must be non-negative"
+    assert call(G(out_form=_lib.LC_GEMV_OUT_SWIGLU), rows=6)[0] == _lib.LC_ERR_INVALID
+    rope = dict(out_form=_lib.LC_GEMV_OUT_ROPE_QKV, q_heads=2, kv_heads=1, head_dim=16,
+                rope_row=16, k_out=16, v_out=16)
+    assert "rows = (q_heads + 2 kv_heads) head_dim" in call(G(**rope), rows=48)[1]
+    assert "head_dim % 16 == 0" in call(G(**dict(rope, head_dim=8)), rows=32)[1]
+    assert call(G(**dict(rope, k_out=None)), rows=64)[1] == \
+        "rope form needs rope_row, k_out and v_out"
 
 
 def test_decode_workspace_checks(lib):

@@ -234,6 +234,161 @@ def test_gemv_single_token(ly, gpu, rows, cols, stride):
     assert np.all(np.abs(got - want) <= bound + 1e-30)
 
 
+def _rand_bf16(torch, g, shape, scale=1.0, shift=0.0):
+    return (shift + scale * torch.randn(*shape, generator=g, device="cuda")).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 512), (33, 4096), (1001, 200), (70, 2056),
+                                       (40000, 1024)])
+@pytest.mark.parametrize("form", ["bf16", "f32", "norm", "norm_res"])
+def test_gemv_fused_input_forms_bit_identical(ly, gpu, rows, cols, form):
+    """lc_gemv_fused's input forms against the unfused calls they fold (lc_gemv
+    after a bf16 cast, after lc_rmsnorm with or without the residual add): the
+    same bits.  200 and 1024 columns take the two-chunk sum-of-squares order,
+    2056 and 4096 the eight-chunk one; 40,000 rows (10,000 row blocks) loop
+    each workgroup of the capped normalising grid over several blocks."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows * 7 + cols)
+    w = _rand_bf16(torch, g, (rows, cols), 0.05)
+    x32 = torch.randn(1, cols, generator=g, device="cuda")
+    x = x32.to(torch.bfloat16)
+    if form == "bf16":
+        got, want = ly.gemv_fused(x, w), ly.linear(x, w)
+    elif form == "f32":
+        got, want = ly.gemv_fused(x32, w), ly.linear(x32.to(torch.bfloat16), w)
+    else:
+        nw = _rand_bf16(torch, g, (cols,), 0.1, 1.0)
+        res = _rand_bf16(torch, g, (1, cols)) if form == "norm_res" else None
+        ro_got = torch.empty_like(x) if res is not None else None
+        ro_want = torch.empty_like(x) if res is not None else None
+        got = ly.gemv_fused(x, w, norm_weight=nw, eps=1e-5, residual=res, residual_out=ro_got)
+        want = ly.linear(ly.rmsnorm(x, nw, 1e-5, residual=res, residual_out=ro_want), w)
+        if res is not None:
+            torch.cuda.synchronize()
+            assert torch.equal(ro_got, ro_want)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape == (1, rows)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("inter,cols,norm", [(14336, 4096, True), (1000, 512, False),
+                                             (8, 64, True), (3000, 200, False)])
+def test_gemv_fused_swiglu_bit_identical(ly, gpu, inter, cols, norm):
+    """The SwiGLU output form (gate rows then up rows of one weight) against
+    lc_gemv + lc_swiglu of the two halves, with the folded norm of the model's
+    MLP input where ``norm`` is set (the decode step's gate/up projection)."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(inter + cols)
+    w = _rand_bf16(torch, g, (2 * inter, cols), 0.05)
+    x = _rand_bf16(torch, g, (1, cols))
+    if norm:
+        nw, res = _rand_bf16(torch, g, (cols,), 0.1, 1.0), _rand_bf16(torch, g, (1, cols))
+        got = ly.gemv_fused(x, w, norm_weight=nw, eps=1e-5, residual=res, swiglu=True)
+        h = ly.rmsnorm(x, nw, 1e-5, residual=res)
+    else:
+        got, h = ly.gemv_fused(x, w, swiglu=True), x
+    gu = ly.linear(h, w)
+    want = ly.swiglu(gu[:, :inter], gu[:, inter:])
+    torch.cuda.synchronize()
+    assert got.shape == want.shape == (1, inter)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("hq,hkv,d,cols", [(32, 8, 128, 4096), (4, 2, 64, 256), (3, 1, 16, 64)])
+def test_gemv_fused_rope_qkv_bit_identical(ly, gpu, hq, hkv, d, cols):
+    """The RoPE/QKV output form with the folded norm (the decode step's first
+    projection) against lc_rmsnorm, lc_gemv, lc_rope_apply of the q and k
+    columns and the copy of v into the cache: q, the cache's k and v rows of
+    the token bit for bit, every other cache row untouched."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(hq * 100 + d)
+    rows = (hq + 2 * hkv) * d
+    w = _rand_bf16(torch, g, (rows, cols), 0.05)
+    x, res = _rand_bf16(torch, g, (1, cols)), _rand_bf16(torch, g, (1, cols))
+    nw = _rand_bf16(torch, g, (cols,), 0.1, 1.0)
+    cap, pos = 50, 37
+    table = ly.rope_table(ly.rope_params(d, 500000.0), cap, 0)
+    kc = torch.zeros(1, cap, hkv, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    xin = torch.empty_like(x)
+    q = ly.gemv_fused(x, w, norm_weight=nw, eps=1e-5, residual=res, residual_out=xin,
+                      rope_row=table[pos], heads=(hq, hkv), k_out=kc[0, pos], v_out=vc[0, pos])
+    xin_w = torch.empty_like(x)
+    qkv = ly.linear(ly.rmsnorm(x, nw, 1e-5, residual=res, residual_out=xin_w), w)
+    qw = ly.rope_apply(qkv[:, :hq * d], table[pos:pos + 1], hq, d)
+    kw = ly.rope_apply(qkv[:, hq * d:(hq + hkv) * d], table[pos:pos + 1], hkv, d)
+    torch.cuda.synchronize()
+    assert torch.equal(xin, xin_w)
+    assert torch.equal(q.view(-1), qw.view(-1))
+    assert torch.equal(kc[0, pos].reshape(-1), kw.view(-1))
+    assert torch.equal(vc[0, pos].reshape(-1), qkv[0, (hq + hkv) * d:])
+    others = torch.ones(cap, dtype=torch.bool)
+    others[pos] = False
+    assert not kc[0, others].any() and not vc[0, others].any()
+
+
+def test_decode_step_fused_equals_unfused(ly, gpu):
+    """The whole decode step with every projection's row operation folded
+    (five launches per layer with the attention) against the unfused
+    sequence: identical logits and caches over several tokens of a 2-layer
+    GQA model."""
+    import torch
+
+    cfg = ly.ModelConfig(hidden_size=512, num_heads=4, num_key_value_heads=2,
+                         intermediate_size=1024, num_layers=2, vocab_size=1000,
+                         rope_theta=500000.0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    weights = ly.init_model_weights(cfg, gen, "cuda", std=0.05)
+    T, extra = 200, 3
+    ids = torch.randint(0, cfg.vocab_size, (T + extra,), generator=gen, device="cuda")
+    table = ly.rope_table(ly.rope_params(cfg.head_dim, cfg.rope_theta), T + extra, 0)
+    caches = [ly.new_cache(cfg, T + extra, "cuda") for _ in range(2)]
+    for c in caches:
+        ly.model_prefill(ids[:T], weights, cfg, table[:T], c)
+    for step in range(extra):
+        pos = T + step
+        a = ly.model_decode_step(int(ids[pos]), pos, weights, cfg, table, caches[0], fused=True)
+        b = ly.model_decode_step(int(ids[pos]), pos, weights, cfg, table, caches[1], fused=False)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), step
+        for (k0, v0), (k1, v1) in zip(*caches):
+            assert torch.equal(k0, k1) and torch.equal(v0, v1), step
+
+
+def test_gemv_fused_rejects_bad_forms(ly, gpu):
+    """lc_gemv_fused validates the forms and their arguments before a launch."""
+    import torch
+
+    bf = torch.bfloat16
+    w = torch.zeros(48, 64, dtype=bf, device="cuda")
+    x = torch.zeros(1, 64, dtype=bf, device="cuda")
+    with pytest.raises(ValueError, match="rows .2 x intermediate. % 4"):
+        ly.gemv_fused(x, torch.zeros(6, 64, dtype=bf, device="cuda"), swiglu=True)
+    table = ly.rope_table(ly.rope_params(16, 10000.0), 4, 0)
+    kv = torch.zeros(1, 16, dtype=bf, device="cuda")
+    with pytest.raises(ValueError, match="rows = .q_heads . 2 kv_heads. head_dim"):
+        ly.gemv_fused(x, torch.zeros(50, 64, dtype=bf, device="cuda"), rope_row=table[0],
+                      heads=(1, 1), k_out=kv, v_out=kv)
+    with pytest.raises(ValueError, match="k_out must be"):
+        ly.gemv_fused(x, w, rope_row=table[0], heads=(1, 1),
+                      k_out=torch.zeros(1, 8, dtype=bf, device="cuda"), v_out=kv)
+    with pytest.raises(ValueError, match="cols <= 4096"):
+        big = torch.zeros(1, 4104, dtype=bf, device="cuda")
+        ly.gemv_fused(big, torch.zeros(4, 4104, dtype=bf, device="cuda"),
+                      norm_weight=torch.ones(4104, dtype=bf, device="cuda"))
+    with pytest.raises(ValueError, match="folded rmsnorm takes a bf16 x"):
+        ly.gemv_fused(x.float(), w, norm_weight=torch.ones(64, dtype=bf, device="cuda"))
+    with pytest.raises(ValueError, match="belong to the folded rmsnorm"):
+        ly.gemv_fused(x, w, residual=x)
+
+
 def test_wrappers_reject_mis_sized_buffers(ly, gpu):
     """The layer kernels take raw pointers: the wrappers check caller-supplied
     outputs, residuals, weights and tables before a launch could overrun them."""
