@@ -19,9 +19,18 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 4;
+constexpr int kPlainRows = 4;
 constexpr int kUnroll = 4;
-constexpr int kSplit = 4;  // waves per workgroup, each over 1/kSplit of the row
+constexpr int kPlainSplit = 4;  // waves per workgroup, each over 1/kPlainSplit of the row
+// The fused forms: four rows per workgroup (their row maps pair rows for
+// SwiGLU and RoPE), kSplit waves over each row.
+constexpr int kRows = 4;
+constexpr int kSplit = 4;
+// Each lane sums its chunks in increasing order whatever the rows per
+// workgroup and the unroll; the split of a row over waves and the order of the
+// wave sums are the rest of the reduction order, so the fused forms equal
+// lc_gemv bit for bit only with the same split.
+static_assert(kSplit == kPlainSplit, "fused and plain kernels reduce in the same order");
 
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
@@ -38,34 +47,34 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
   return acc;
 }
 
-__global__ __launch_bounds__(64 * kSplit) void gemv_bf16_kernel(int64_t n, int k,
+__global__ __launch_bounds__(64 * kPlainSplit) void gemv_bf16_kernel(int64_t n, int k,
                                                                  const uint16_t* w, int64_t ws,
                                                                  const uint16_t* x, uint16_t* y) {
-  __shared__ float part[kSplit][kRows];
+  __shared__ float part[kPlainSplit][kPlainRows];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t row0 = (int64_t)blockIdx.x * kRows;
+  const int64_t row0 = (int64_t)blockIdx.x * kPlainRows;
   const int nch = k / 8;  // 16-byte chunks per row
-  const int per = (nch + kSplit - 1) / kSplit;
+  const int per = (nch + kPlainSplit - 1) / kPlainSplit;
   const int cb = wave * per;
   const int ce = min(nch, cb + per);
   const uint4* xv = reinterpret_cast<const uint4*>(x);
-  const uint4* wr[kRows];
+  const uint4* wr[kPlainRows];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
+  for (int r = 0; r < kPlainRows; ++r) {
     const int64_t row = row0 + r < n ? row0 + r : n - 1;  // tail rows re-read the last one
     wr[r] = reinterpret_cast<const uint4*>(w + row * ws);
   }
-  float acc[kRows] = {};
+  float acc[kPlainRows] = {};
   for (int c0 = cb; c0 < ce; c0 += 64 * kUnroll) {
-    uint4 xc[kUnroll], wc[kRows][kUnroll];
+    uint4 xc[kUnroll], wc[kPlainRows][kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int c = c0 + 64 * u + lane;
       const bool in = c < ce;
       xc[u] = in ? xv[c] : uint4{0, 0, 0, 0};
 #pragma unroll
-      for (int r = 0; r < kRows; ++r) {  // weights stream once per token: non-temporal
+      for (int r = 0; r < kPlainRows; ++r) {  // weights stream once per token: non-temporal
         const u32x4 v = in ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&wr[r][c]))
                            : u32x4{0, 0, 0, 0};
         wc[r][u] = uint4{v[0], v[1], v[2], v[3]};
@@ -74,21 +83,21 @@ __global__ __launch_bounds__(64 * kSplit) void gemv_bf16_kernel(int64_t n, int k
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-      for (int r = 0; r < kRows; ++r) acc[r] = dot8(wc[r][u], xc[u], acc[r]);
+      for (int r = 0; r < kPlainRows; ++r) acc[r] = dot8(wc[r][u], xc[u], acc[r]);
   }
 #pragma unroll
-  for (int r = 0; r < kRows; ++r)
+  for (int r = 0; r < kPlainRows; ++r)
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) part[wave][r] = acc[r];
+    for (int r = 0; r < kPlainRows; ++r) part[wave][r] = acc[r];
   }
   __syncthreads();
-  if (threadIdx.x < kRows && row0 + threadIdx.x < n) {
+  if (threadIdx.x < kPlainRows && row0 + threadIdx.x < n) {
     float v = 0.f;
 #pragma unroll
-    for (int i = 0; i < kSplit; ++i) v += part[i][threadIdx.x];
+    for (int i = 0; i < kPlainSplit; ++i) v += part[i][threadIdx.x];
     y[row0 + threadIdx.x] = f32_to_bf16(v);
   }
 }
@@ -453,8 +462,8 @@ hipError_t launch_gemv_fused(int in_form, int out_form, int64_t rows, int cols, 
 
 hipError_t launch_gemv_bf16(int64_t n, int k, const void* w, int64_t ws, const void* x, void* y,
                             hipStream_t s) {
-  const int64_t grid = (n + kRows - 1) / kRows;
-  hipLaunchKernelGGL(gemv_bf16_kernel, dim3((unsigned)grid), dim3(64 * kSplit), 0, s, n, k,
+  const int64_t grid = (n + kPlainRows - 1) / kPlainRows;
+  hipLaunchKernelGGL(gemv_bf16_kernel, dim3((unsigned)grid), dim3(64 * kPlainSplit), 0, s, n, k,
                      static_cast<const uint16_t*>(w), ws, static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(y));
   return hipGetLastError();
