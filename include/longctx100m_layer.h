@@ -107,7 +107,9 @@ int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_
  *   LC_GEMV_IN_RMSNORM  x is bf16 [cols]; the vector is lc_rmsnorm of the one
  *                       row x (+ residual) with norm_weight and eps, and
  *                       x + residual is written to residual_out when that is
- *                       set (cols <= 4096).
+ *                       set (cols <= 4096; residual_out must not overlap x or
+ *                       residual: one workgroup writes it while the others
+ *                       still read them).
  * Output forms:
  *   LC_GEMV_OUT_PLAIN     y [rows], as lc_gemv;
  *   LC_GEMV_OUT_SWIGLU    rows = 2 I (gate rows, then up rows, as one fused

@@ -198,6 +198,16 @@ int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const vo
           (f->residual_out && !aligned16(f->residual_out)))
         return set_error(LC_ERR_INVALID, "rmsnorm pointers must be 16-byte aligned");
       if (!(f->eps >= 0.f)) return set_error(LC_ERR_INVALID, "eps must be non-negative");
+      if (f->residual_out) {  // written by one workgroup while the others read x and residual
+        const auto lo = reinterpret_cast<uintptr_t>(f->residual_out);
+        const auto hi = lo + 2 * (uintptr_t)cols;
+        auto overlaps = [&](const void* p) {
+          const auto b = reinterpret_cast<uintptr_t>(p);
+          return b < hi && lo < b + 2 * (uintptr_t)cols;
+        };
+        if (overlaps(x) || overlaps(f->residual))
+          return set_error(LC_ERR_INVALID, "residual_out must not overlap x or residual");
+      }
       break;
     default:
       return set_error(LC_ERR_INVALID, "unknown gemv input form %d", f->in_form);

@@ -211,6 +211,12 @@ def test_gemv_fused_argument_errors(lib):
         "rmsnorm pointers must be 16-byte aligned"
     assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, eps=-1.0))[1] == \
         "eps must be non-negative"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, residual=4096,
+                  residual_out=16 + 64))[1] == "residual_out must not overlap x or residual"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, residual=4096,
+                  residual_out=4096 + 112))[1] == "residual_out must not overlap x or residual"
+    assert call(G(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, residual=4096,
+                  residual_out=16 + 128))[0] == _lib.LC_OK  # adjacent, rows = 0: no launch
     assert call(G(out_form=_lib.LC_GEMV_OUT_SWIGLU), rows=6)[0] == _lib.LC_ERR_INVALID
     rope = dict(out_form=_lib.LC_GEMV_OUT_ROPE_QKV, q_heads=2, kv_heads=1, head_dim=16,
                 rope_row=16, k_out=16, v_out=16)
