@@ -1,6 +1,6 @@
 /*
  * A C caller of liblongctx100m_attn: binds include/longctx100m_attn.h the way
- * a non-Python FFI (the reference's Rust crate) would, with
+ * a non-Python FFI (such as the reference's Rust crate) would, with
  * plain pointers and the host-pointer entry points of the reference's ring
  * signatures (ring_attention.rs:139-233 and :281-475).
  *
