@@ -362,6 +362,70 @@ def test_decode_step_fused_equals_unfused(ly, gpu):
             assert torch.equal(k0, k1) and torch.equal(v0, v1), step
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_gemv_fused_random_shapes(ly, gpu, seed):
+    """Seeded random shapes through every input x output form combination
+    lc_gemv_fused accepts, each against the unfused calls it folds, bit for
+    bit: cols any multiple of 8 up to 4096 (up to 9000 without the norm),
+    rows with ragged row blocks, GQA head counts and head dims of 16 to 256."""
+    import torch
+
+    rng = np.random.default_rng(1000 + seed)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    in_form = ["bf16", "f32", "norm", "norm_res"][seed % 4]
+    out_form = ["plain", "swiglu", "rope"][(seed // 4) % 3]
+    cols = 8 * int(rng.integers(1, (4096 if in_form.startswith("norm") else 9000) // 8 + 1))
+    if out_form == "rope":
+        d = 16 * int(rng.integers(1, 17))
+        hkv = int(rng.integers(1, 5))
+        hq = hkv * int(rng.integers(1, 5))
+        rows = (hq + 2 * hkv) * d
+    elif out_form == "swiglu":
+        rows = 2 * 8 * int(rng.integers(1, 700))
+    else:
+        rows = int(rng.integers(1, 9000))
+    w = _rand_bf16(torch, g, (rows, cols), 0.05)
+    x32 = torch.randn(1, cols, generator=g, device="cuda")
+    x = x32.to(torch.bfloat16)
+    kw, ro_got, ro_want, res, nw = {}, None, None, None, None
+    if in_form.startswith("norm"):
+        nw = _rand_bf16(torch, g, (cols,), 0.1, 1.0)
+        if in_form == "norm_res":
+            res = _rand_bf16(torch, g, (1, cols))
+            ro_got, ro_want = torch.empty_like(x), torch.empty_like(x)
+        kw = dict(norm_weight=nw, eps=1e-6, residual=res, residual_out=ro_got)
+        h = ly.rmsnorm(x, nw, 1e-6, residual=res, residual_out=ro_want)
+        xin = x
+    elif in_form == "f32":
+        xin, h = x32, x
+    else:
+        xin, h = x, x
+    if out_form == "plain":
+        got = ly.gemv_fused(xin, w, **kw)
+        want = ly.linear(h, w)
+        checks = [(got, want)]
+    elif out_form == "swiglu":
+        got = ly.gemv_fused(xin, w, swiglu=True, **kw)
+        gu = ly.linear(h, w)
+        want = ly.swiglu(gu[:, :rows // 2], gu[:, rows // 2:])
+        checks = [(got, want)]
+    else:
+        table = ly.rope_table(ly.rope_params(d, 10000.0), 5, 100)
+        kc = torch.zeros(hkv * d, dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        got = ly.gemv_fused(xin, w, rope_row=table[2], heads=(hq, hkv), k_out=kc, v_out=vc, **kw)
+        qkv = ly.linear(h, w)
+        qw = ly.rope_apply(qkv[:, :hq * d], table[2:3], hq, d)
+        kw_ = ly.rope_apply(qkv[:, hq * d:(hq + hkv) * d], table[2:3], hkv, d)
+        checks = [(got.view(-1), qw.view(-1)), (kc, kw_.view(-1)), (vc, qkv[0, (hq + hkv) * d:])]
+    torch.cuda.synchronize()
+    for a, b in checks:
+        assert a.shape == b.shape and torch.equal(a, b), (in_form, out_form, rows, cols)
+    if ro_got is not None:
+        assert torch.equal(ro_got, ro_want)
+
+
 def test_gemv_fused_rejects_bad_forms(ly, gpu):
     """lc_gemv_fused validates the forms and their arguments before a launch."""
     import torch
