@@ -124,7 +124,8 @@ int lc_gemv(int32_t dtype, int64_t rows, int32_t cols, const void* w, int64_t w_
  *                         and <= 256 (as lc_rope_apply).  k_out and v_out may be the token's rows
  *                         of a KV cache.
  * bf16 weights only; cols and w_stride multiples of 8, w_stride >= cols; w,
- * x, residual, residual_out and norm_weight 16-byte aligned. */
+ * x, residual, residual_out and norm_weight 16-byte aligned, rope_row 4-byte,
+ * y, k_out and v_out 2-byte aligned. */
 #define LC_GEMV_IN_BF16 0
 #define LC_GEMV_IN_F32 1
 #define LC_GEMV_IN_RMSNORM 2

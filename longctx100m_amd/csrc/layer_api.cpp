@@ -184,6 +184,8 @@ int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const vo
     return set_error(LC_ERR_INVALID, "row strides must be >= cols and multiples of 8 elements");
   if (!aligned16(w) || !aligned16(x))
     return set_error(LC_ERR_INVALID, "gemv w and x must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(y) & 1u)
+    return set_error(LC_ERR_INVALID, "gemv y must be 2-byte aligned");
   switch (f->in_form) {
     case LC_GEMV_IN_BF16:
     case LC_GEMV_IN_F32:
@@ -227,6 +229,9 @@ int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const vo
         return set_error(LC_ERR_INVALID, "rope form needs rows = (q_heads + 2 kv_heads) head_dim");
       if (!f->rope_row || !f->k_out || !f->v_out)
         return set_error(LC_ERR_INVALID, "rope form needs rope_row, k_out and v_out");
+      if ((reinterpret_cast<uintptr_t>(f->rope_row) & 3u) ||
+          (reinterpret_cast<uintptr_t>(f->k_out) & 1u) || (reinterpret_cast<uintptr_t>(f->v_out) & 1u))
+        return set_error(LC_ERR_INVALID, "rope_row must be 4-byte and k_out, v_out 2-byte aligned");
       break;
     default:
       return set_error(LC_ERR_INVALID, "unknown gemv output form %d", f->out_form);

@@ -224,6 +224,10 @@ def test_gemv_fused_argument_errors(lib):
     assert "head_dim % 16 == 0" in call(G(**dict(rope, head_dim=8)), rows=32)[1]
     assert call(G(**dict(rope, k_out=None)), rows=64)[1] == \
         "rope form needs rope_row, k_out and v_out"
+    assert call(G(**dict(rope, rope_row=18)), rows=64)[1] == \
+        "rope_row must be 4-byte and k_out, v_out 2-byte aligned"
+    assert call(G(**dict(rope, v_out=17)), rows=64)[1] == \
+        "rope_row must be 4-byte and k_out, v_out 2-byte aligned"
 
 
 def test_decode_workspace_checks(lib):
