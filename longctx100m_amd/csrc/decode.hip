@@ -221,20 +221,25 @@ __global__ __launch_bounds__(64) void decode128_kernel(DecodeArgs a) {
   }
 }
 
-// Log-sum-exp merge of the S split partials of each row: one 1024-thread
-// workgroup per row (b, i, h) = ((b * Nq) + i) * Hq + h of o.  A decode step
-// has only B * Nq * Hq rows, too few workgroups to hide latency, so the
-// kernel keeps its chains short: one round of statistics loads (each thread
-// holds the (m, l) of up to four splits), the max M and the sum L of the
-// split weights w_s = l_s * exp(m_s - M) reduced by wave shuffles and one LDS
-// exchange each, then thread (d, g) sums w_s * o_s[d] over the splits
-// s = g mod 8 and the eight group sums meet in LDS.  m and l are written in
-// the [B, Hq, Nq] layout of the statistics.
+// Log-sum-exp merge of the S split partials of each row (b, i, h) =
+// ((b * Nq) + i) * Hq + h of o.  A decode step has only B * Nq * Hq rows, so
+// each row's D dims are split over kMergeParts 1024-thread workgroups (four
+// per row: 128 workgroups for the 32 rows of a GQA 32/8 token) and every
+// chain is short: one round of statistics loads (each thread holds the (m, l)
+// of up to four splits; every workgroup of a row forms all split weights),
+// the max M and the sum L of the weights w_s = l_s * exp(m_s - M) reduced by
+// wave shuffles and one LDS exchange each, then thread (d, g) of the
+// workgroup's D / kMergeParts dims sums w_s * o_s[d] over the splits
+// s = g mod kMergeGroups and the group sums meet in LDS.  m and l (written by
+// the first workgroup of the row) use the [B, Hq, Nq] layout of the
+// statistics.
 constexpr int kMergeMaxSplits = 4096;
 constexpr int kMergeThreads = 1024;
 constexpr int kMergePer = kMergeMaxSplits / kMergeThreads;  // splits per thread
 constexpr int kMergeWaves = kMergeThreads / 64;
-constexpr int kMergeGroups = kMergeThreads / D;
+constexpr int kMergeParts = 4;                        // workgroups per row
+constexpr int kMergeDims = D / kMergeParts;           // dims per workgroup
+constexpr int kMergeGroups = kMergeThreads / kMergeDims;
 
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     int64_t nrows, int S, int Nq, int Hq, const float* o_part, const float* m_part,
@@ -245,7 +250,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   __shared__ float part[kMergeThreads];
   const int t = threadIdx.x;
   const int wave = t >> 6;
-  const int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.x / kMergeParts;
+  const int d0 = (int)(blockIdx.x % kMergeParts) * kMergeDims;
   float ms[kMergePer], ls[kMergePer];
   float mx = -INFINITY;
 #pragma unroll
@@ -275,24 +281,25 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   float L = 0.f;
 #pragma unroll
   for (int i = 0; i < kMergeWaves; ++i) L += wave_sum[i];
-  // weighted sum of the partial outputs: thread (d, g) over splits g, g + 8, ...
-  const int d = t & (D - 1);
-  const int g = t / D;
+  // weighted sum of the partial outputs: thread (d, g) over splits g, g + kMergeGroups, ...
+  const int dd = t % kMergeDims;
+  const int d = d0 + dd;
+  const int g = t / kMergeDims;
   float acc = 0.f;  // partials of empty splits are zeros with zero weight
   const float* op = o_part + row * D + d;
-  const int64_t sstride = (int64_t)kMergeGroups * nrows * D;
+  const int64_t sstride = (int64_t)nrows * D;
 #pragma unroll 4
-  for (int sp = g; sp < S; sp += kMergeGroups)
-    acc = fmaf(w[sp], op[(int64_t)(sp / kMergeGroups) * sstride + (int64_t)g * nrows * D], acc);
+  for (int sp = g; sp < S; sp += kMergeGroups) acc = fmaf(w[sp], op[(int64_t)sp * sstride], acc);
   part[t] = acc;
   __syncthreads();
   if (g == 0) {
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMergeGroups; ++i) sum += part[i * D + d];
+    for (int i = 0; i < kMergeGroups; ++i) sum += part[i * kMergeDims + dd];
     const float inv = L > 0.f ? 1.f / L : 0.f;
     o[row * D + d] = sum * inv;
   }
+  if (d0 != 0) return;  // the row's statistics come from its first workgroup
   if (t == 0) {
     const int h = (int)(row % Hq);
     const int64_t bi = row / Hq;
@@ -380,7 +387,7 @@ hipError_t launch_decode128(const Problem& p, const void* q, const void* k, cons
   hipLaunchKernelGGL(decode128_kernel, dim3((unsigned)(S * p.Hkv * p.B)), dim3(64), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)rows), dim3(kMergeThreads), 0, st,
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(rows * kMergeParts)), dim3(kMergeThreads), 0, st,
                      rows, S, p.Nq, p.Hq, o_part, m_part, l_part, o, m, l);
   return hipGetLastError();
 }
