@@ -623,7 +623,14 @@ def other_configs(torch, ra) -> dict:
     out = {}
     for name, (fn, steps, warmup) in OTHER_CONFIGS.items():
         t0 = time.perf_counter()
-        line = fn(torch, ra, steps, warmup)
+        try:
+            line = fn(torch, ra, steps, warmup)
+        except (RuntimeError, ValueError) as e:  # e.g. out of memory: the headline still prints
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            out[name] = {"error": f"{type(e).__name__}: {e}"[:300]}
+            log(f"{name}: failed ({out[name]['error']})")
+            continue
         torch.cuda.empty_cache()
         out[name] = {k: line[k] for k in SUMMARY_KEYS if k in line}
         out[name]["wall_s"] = round(time.perf_counter() - t0, 1)
