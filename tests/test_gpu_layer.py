@@ -273,6 +273,22 @@ def test_gemv_fused_input_forms_bit_identical(ly, gpu, rows, cols, form):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("rows,cols", [(70, 14336), (4096, 8200), (9, 16384)])
+def test_gemv_fused_long_rows_bit_identical(ly, gpu, rows, cols):
+    """Rows longer than 8192 columns: lc_gemv takes several rounds of four
+    chunks per lane, the fp32-input form several rounds of two; both sum each
+    lane's chunks in the same order, so the results are the same bits."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows + cols)
+    w = _rand_bf16(torch, g, (rows, cols), 0.05)
+    x32 = torch.randn(1, cols, generator=g, device="cuda")
+    got, want = ly.gemv_fused(x32, w), ly.linear(x32.to(torch.bfloat16), w)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("inter,cols,norm", [(14336, 4096, True), (1000, 512, False),
                                              (8, 64, True), (3000, 200, False)])
 def test_gemv_fused_swiglu_bit_identical(ly, gpu, inter, cols, norm):
