@@ -43,9 +43,11 @@ COMMON_FLAGS = [
 
 
 # Per-source extras.  layer.hip restates the reference's separately rounded
-# tensor ops, so nothing in it may be contracted into fused multiply-adds.
+# tensor ops, and gemv.hip folds the same ops into the decode projections, so
+# nothing in either may be contracted into fused multiply-adds.
 EXTRA_FLAGS = {
     "layer.hip": ["-ffp-contract=off"],
+    "gemv.hip": ["-ffp-contract=off"],
 }
 
 

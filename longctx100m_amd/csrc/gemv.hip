@@ -14,6 +14,15 @@
 #include "common.h"
 #include "kernels.h"
 
+// The folded row operations round every product and sum on their own, as
+// layer.hip's stand-alone kernels do: no contraction into fused multiply-adds
+// in this file (the build also passes -ffp-contract=off for it).  The _rn
+// intrinsics alone do not ensure that: without OCML_BASIC_ROUNDED_OPERATIONS
+// they are plain operators, which contraction fuses once inlined (one RoPE
+// output in thousands came out an ulp apart).  The dot products use explicit
+// fmaf and are unaffected.
+#pragma clang fp contract(off)
+
 namespace lc {
 namespace {
 
