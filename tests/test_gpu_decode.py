@@ -71,6 +71,33 @@ def test_decode_matches_dense(ra, gpu, case):
     _check(o, m, l, eo, em, el)
 
 
+def _random_decode_cases(seed, n):
+    """Random decode geometries (drawn once), in DECODE_CASES' tuple form: batch,
+    1-4 new tokens, GQA groups up to 8 (16 or fewer rows per KV head take the
+    split kernel, more the blockwise fallback), caches of 1 to 20,000 keys at
+    an offset, queries anywhere from before the first key to the cache end,
+    causal or not, valid_length inside or past the cache."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        hkv = int(rng.choice([1, 2, 4]))
+        nq = int(rng.integers(1, 5))
+        nk = int(rng.integers(1, 20001))
+        kp = int(rng.choice([0, int(rng.integers(0, 300000))]))
+        qoff = -int(rng.integers(0, min(nk, 50) + 1)) if rng.integers(0, 3) else 0
+        valid = None if rng.integers(0, 3) else int(rng.integers(1, kp + nk + 100))
+        out.append((int(rng.integers(1, 3)), nq, hkv * int(rng.choice([1, 2, 4, 8])), hkv, nk,
+                    qoff, kp, bool(rng.integers(0, 4)), valid))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_decode_cases(77, 24))
+def test_decode_random_against_dense(ra, gpu, case):
+    """Seeded random decode geometries through lc_attn_decode against the fp64
+    dense oracle, at the bars of DECODE_CASES."""
+    test_decode_matches_dense(ra, gpu, case)
+
+
 def test_decode_equals_fwd_shard(ra, gpu):
     """Both entry points give the same statistics for the same decode step."""
     rng = np.random.default_rng(77)
