@@ -921,3 +921,33 @@ def test_random_shapes_fwd_and_shared_ds_bwd(ra, gpu, case):
     assert norm_rel(_np(dq), edq) <= BF16_TOL
     assert norm_rel(_np(dk), edk) <= BF16_TOL
     assert norm_rel(_np(dv), edv) <= BF16_TOL
+
+
+@pytest.mark.parametrize("case", _random_cases(2031, 10), ids=lambda c: "q{nq}k{nk}h{hq}/{hkv}".format(**c))
+def test_random_shapes_shared_ds_partial_workspace(ra, gpu, case):
+    """The dS-sharing backward with a workspace smaller than the whole shard
+    pair's dS: the pair runs in query chunks of multiples of 256 rows, or, below
+    one chunk, the recomputing dQ kernel.  Random shapes and a random fraction
+    (0 to 0.8) of the full workspace, against the fp64 dense oracle."""
+    c = dict(case)
+    b, nq, nk, hq, hkv = c.pop("b"), c.pop("nq"), c.pop("nk"), c.pop("hq"), c.pop("hkv")
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()) + 1)
+    q = _t(gpu, rng.standard_normal((b, nq, hq, 128)), gpu.bfloat16)
+    k = _t(gpu, rng.standard_normal((b, nk, hkv, 128)), gpu.bfloat16)
+    v = _t(gpu, rng.standard_normal((b, nk, hkv, 128)), gpu.bfloat16)
+    do = _t(gpu, rng.standard_normal((b, nq, hq, 128)), gpu.bfloat16)
+    o32, m, l = ra.fwd_shard(q, k, v, **c)
+    out = o32.to(gpu.bfloat16)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    full = ra.bwd_shard_workspace_bytes(q, k)
+    nbytes = max(256, int(full * float(rng.choice([0.0, 0.2, 0.4, 0.6, 0.8]))) // 256 * 256)
+    ws = gpu.empty(nbytes, dtype=gpu.uint8, device="cuda")
+    dq = gpu.zeros((b, nq, hq, 128), dtype=gpu.float32, device="cuda")
+    dk = gpu.zeros((b, nk, hkv, 128), dtype=gpu.float32, device="cuda")
+    dv = gpu.zeros_like(dk)
+    ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, workspace=ws, **c)
+    gpu.cuda.synchronize()
+    edq, edk, edv = dense.attention_bwd(_np(q), _np(k), _np(v), _np(do), out=_np(out), **c)
+    assert norm_rel(_np(dq), edq) <= BF16_TOL
+    assert norm_rel(_np(dk), edk) <= BF16_TOL
+    assert norm_rel(_np(dv), edv) <= BF16_TOL
