@@ -3,7 +3,8 @@ and of one composed layer against the numpy oracle (oracle/layer.py, with
 oracle/dense.py for the attention).
 
 Bars: bf16 results within one bf16 ulp of the oracle (2^-7 relative, the two
-roundings the reference makes can each land on the other side), fp32 within
+roundings the reference makes can each land on the other side; for RMSNorm a
+few elements in 10^5 within two, from the fp32 sum of squares), fp32 within
 2e-6 relative; RoPE given the same table and the fused residual add are
 bit-exact; the composed bf16 layer within 2e-2 norm-relative.
 """
@@ -36,15 +37,18 @@ def _np(t):
 
 
 def _close(got, want, dtype, rare=0.0):
-    """bf16: within one ulp; with rare > 0 a fraction <= rare of the elements may
-    be within two (large samples: a sum of squares rounded differently moves
-    h * inv across a rounding boundary, and the second rounding can add to it)."""
+    """bf16: within one ulp; with rare > 0 up to rare * size + 2 elements may be
+    within two (the kernel sums squares in fp32, the oracle in float64: the
+    ~1e-7 difference moves h * inv across a bf16 rounding boundary for ~1e-5
+    of the elements, and the rounding after the weight can add one ulp more;
+    a 300-case random sweep measured up to 1.1e-5)."""
     if dtype == "bf16":
         rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-30)
         far = np.abs(got - want) > 1e-30
         bad = (rel > BF16_ULP) & far
         assert not ((rel > 2 * BF16_ULP) & far).any(), (got[bad][:5], want[bad][:5])
-        assert bad.mean() <= rare, (bad.sum(), got[bad][:5], want[bad][:5])
+        limit = rare * bad.size + (2 if rare > 0 else 0)
+        assert bad.sum() <= limit, (bad.sum(), got[bad][:5], want[bad][:5])
     else:
         np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
 
@@ -81,7 +85,7 @@ def test_rmsnorm(ly, gpu, dtype, rows, cols, with_res):
         out = ly.rmsnorm(xv, tw, 1e-5)
         want, _ = L.rmsnorm(x, w, 1e-5, dtype=dtype)
     gpu.cuda.synchronize()
-    _close(_np(out), want, dtype, rare=1e-5 if rows * cols > 1 << 20 else 0.0)
+    _close(_np(out), want, dtype, rare=5e-5)
 
 
 @pytest.mark.parametrize("scaling", [None, {"rope_type": "linear", "factor": 4.0},
