@@ -229,6 +229,23 @@ def measured_traffic(rl_kernel: str, n: int, h: int, d: int):
     return sum(per[k] for k in names)
 
 
+def algorithmic_bytes(rl_kernel: str, n: int, h: int, d: int) -> int:
+    """HBM bytes the mathematics of one full hop has to move, for the roofline
+    kernel(s): the backward pair reads Q, dO, K, V (bf16) and the two row
+    statistics (LSE, delta; fp32) and read-modify-writes dQ, dK, dV (fp32);
+    the merging forward reads Q, K, V and read-modify-writes the running fp32
+    output and its (m, l).  The dS the dK/dV kernel stores and the dQ kernel
+    reads back (bf16, N x N x H) is a choice of this design, not part of the
+    floor."""
+    bf16_in, f32_row, f32_stat = n * h * d * 2, n * h * d * 4, n * h * 4
+    if rl_kernel.startswith("dkdv128_kernel + dqds128_kernel") or \
+            rl_kernel.startswith("dq128_kernel + dkdv128_kernel"):
+        return 4 * bf16_in + 2 * f32_stat + 3 * 2 * f32_row
+    if rl_kernel.startswith("fwd128_kernel"):
+        return 3 * bf16_in + 2 * f32_row + 2 * 2 * f32_stat
+    return 0
+
+
 def long_shard_line(torch, ra, steps: int, warmup: int) -> dict:
     """rank 1 of a 2-shard layout with 1,000,000 local tokens,
     Hq = Hkv = 16, d = 128, bf16; forward over the diagonal block and one full
@@ -287,19 +304,22 @@ def long_shard(args, torch, ra) -> int:
     return 0
 
 
-def host_path(args, torch, ra) -> int:
-    """The reference's signatures on host memory (lc_ring_fwd_with_stats_host,
+def host_path_line(torch, ra, steps: int, warmup: int, n: int = 32768, h: int = 16,
+                   d: int = 128, world: int = 8, rank: int = 7) -> dict:
+    """The reference's signatures (ring_causal_attention_forward_with_stats,
+    ring_causal_attention_backward: rs:139-233, rs:281-475) at configs 2/3
+    shapes: on shards already in HBM (lc_ring_fwd_with_stats, then lc_ring_bwd
+    with the workspace of lc_ring_bwd_ds_workspace_bytes, which shares dS on
+    the diagonal pair), and on host memory (lc_ring_fwd_with_stats_host,
     lc_ring_bwd_host: every call copies all ranks' shards to HBM and the
-    results back) against lc_ring_fwd_with_stats / lc_ring_bwd on the same
-    shards already in HBM, rank 7 of 8, 32,768-token bf16 shards, 16/16 heads,
-    d = 128.  Both run the same kernels; the difference is the PCIe traffic."""
+    results back).  Both run the same kernels; the difference is the PCIe
+    traffic.  value = device-resident forward + backward, ms per call."""
     import ctypes
 
     import numpy as np
 
     from longctx100m_amd import _lib
 
-    n, h, d, world, rank = args.tokens, args.heads, args.head_dim, args.world, args.rank
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
@@ -350,7 +370,7 @@ def host_path(args, torch, ra) -> int:
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / reps
 
-    reps = max(1, min(args.steps, 3))
+    reps = max(1, steps)
     res = {"fwd_host_s": wall(fwd_host, reps), "fwd_device_s": wall(fwd_dev, reps),
            "bwd_host_s": wall(bwd_host, reps), "bwd_device_s": wall(bwd_dev, reps)}
     shard = n * h * d * 2
@@ -358,8 +378,11 @@ def host_path(args, torch, ra) -> int:
     fwd_bytes = (1 + 2 * world) * shard + shard + 2 * stat      # Q + all K, V in; out, m, l back
     bwd_bytes = world * (5 * shard + 2 * stat) + 3 * shard      # q, k, v, out, dO, m, l per rank in; dq, dk, dv back
     line = {
-        "metric": "host-pointer ring entry points (PCIe-inclusive) vs device-resident, seconds per call",
-        "unit": "s", "n_gpus": 1, "higher_is_better": False, "dtype": "bf16",
+        "metric": "reference-signature ring fwd+bwd (lc_ring_fwd_with_stats + lc_ring_bwd), "
+                  "device-resident ms per call; host-pointer (PCIe-inclusive) seconds alongside",
+        "value": round(1e3 * (res["fwd_device_s"] + res["bwd_device_s"]), 2),
+        "unit": "ms", "steps": reps, "ms_per_step": round(1e3 * (res["fwd_device_s"] + res["bwd_device_s"]), 2),
+        "n_gpus": 1, "higher_is_better": False, "dtype": "bf16",
         "data": "synthetic: Q, K, V, dO ~ N(0,1), seeded; host copies in pageable memory",
         "config": {"workload": f"BASELINE configs 2/3 shapes through the reference signatures: "
                                f"rank {rank} of {world}, {n}-token shards, Hq=Hkv={h}, d={d}",
@@ -370,7 +393,14 @@ def host_path(args, torch, ra) -> int:
         "effective_copy_GB_per_s": {
             "fwd": round(fwd_bytes / max(res["fwd_host_s"] - res["fwd_device_s"], 1e-9) / 1e9, 1),
             "bwd": round(bwd_bytes / max(res["bwd_host_s"] - res["bwd_device_s"], 1e-9) / 1e9, 1)},
+        "bwd_ds_workspace_bytes": int(lib.lc_ring_bwd_ds_workspace_bytes(ctypes.byref(desc))),
     }
+    return line
+
+
+def host_path(args, torch, ra) -> int:
+    line = host_path_line(torch, ra, max(1, min(args.steps, 3)), 1, args.tokens, args.heads,
+                          args.head_dim, args.world, args.rank)
     print(json.dumps(line), flush=True)
     return 0
 
@@ -429,7 +459,7 @@ def c4_prefill(args, torch, ra) -> int:
     return 0
 
 
-def c4_model(args, torch, ra) -> int:
+def c4_model_line(torch, ra, steps: int, warmup: int) -> dict:
     """the C4 model's prefill on one GPU's share.  Token ids
     of a 65,536-token local shard -> embedding -> 24 decoder layers (RMSNorm,
     fused QKV GEMM, RoPE, ring attention at rank 3 of 4 over the diagonal block
@@ -470,12 +500,12 @@ def c4_model(args, torch, ra) -> int:
         h = ly.rmsnorm(x, final_norm, cfg.rms_norm_eps, residual=res)
         return torch.matmul(h, lm_head.t())
 
-    for _ in range(max(0, min(args.warmup, 1))):
+    for _ in range(warmup):
         prefill()
     torch.cuda.synchronize()
     log("C4 model prefill: warmup done")
     timers = {}
-    steps = max(1, min(args.steps, 2))
+    steps = max(1, steps)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(steps):
@@ -511,6 +541,11 @@ def c4_model(args, torch, ra) -> int:
         "logits_shape": list(logits.shape),
         "hbm_peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
     }
+    return line
+
+
+def c4_model(args, torch, ra) -> int:
+    line = c4_model_line(torch, ra, max(1, min(args.steps, 2)), max(0, min(args.warmup, 1)))
     print(json.dumps(line), flush=True)
     return 0
 
@@ -610,16 +645,20 @@ def c4_decode(args, torch, ra) -> int:
 OTHER_CONFIGS = {
     "c5_long_shard_fwd": (long_shard_line, 1, 1),
     "c4_prefill_attention": (c4_prefill_line, 2, 1),
+    "c4_model_prefill": (c4_model_line, 1, 1),
     "c4_decode": (c4_decode_line, 5, 2),
+    "reference_signature_c2": (host_path_line, 2, 1),
 }
-SUMMARY_KEYS = ("metric", "value", "unit", "higher_is_better", "steps", "ms_per_step",
+SUMMARY_KEYS = ("metric", "value", "unit", "higher_is_better", "steps", "ms_per_step", "tokens_per_s",
+                "fwd_device_s", "bwd_device_s", "fwd_host_s", "bwd_host_s",
                 "pct_mfma_peak", "roofline", "config")
 
 
 def other_configs(torch, ra) -> dict:
     """The other BASELINE configurations that fit one GPU, each a short run:
     the summary of the line its own flag prints (the full line comes from
-    bench.py --long-shard / --c4-prefill / --c4-decode)."""
+    bench.py --long-shard / --c4-prefill / --c4-model / --c4-decode /
+    --host-path)."""
     out = {}
     for name, (fn, steps, warmup) in OTHER_CONFIGS.items():
         t0 = time.perf_counter()
@@ -759,10 +798,19 @@ def main() -> int:
         rl_kernel = "whole step"
         rl_units = f"{total_flops / 1e12:.3f} TFLOP per step"
     sclk = clock.summary()
+    traffic = measured_traffic(rl_kernel, n, h, d)
+    alg_bytes = algorithmic_bytes(rl_kernel, n, h, d)
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": measured_traffic(rl_kernel, n, h, d), "kernel": rl_kernel,
-                "algorithmic": rl_units, "sclk_mhz": sclk,
+                "traffic": traffic, "kernel": rl_kernel,
+                "algorithmic": rl_units,
+                # HBM bytes the mathematics of the hop needs (no dS exchange), and how many
+                # times that the kernels move (the dS round trip is most of the excess)
+                "traffic_algorithmic": alg_bytes or None,
+                "traffic_over_algorithmic": (round(traffic / alg_bytes, 2)
+                                             if traffic and alg_bytes else None),
+                "ds_exchange_bytes": (2 * n * n * h * 2 if "dqds128" in rl_kernel else 0),
+                "sclk_mhz": sclk,
                 # the same fraction against the peak scaled to the mean sampled shader clock
                 # (the 2516.6 TFLOP/s peak assumes 2.4 GHz; the samples are the firmware's
                 # clock levels, so this is approximate): comparable across boxes

@@ -117,7 +117,9 @@ int lc_attn_decode(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, con
  * lc_attn_decode_workspace_bytes exceeds that size are rejected with
  * LC_ERR_WORKSPACE (use lc_attn_decode).  Every call on one GPU shares its
  * array, so calls that overlap on one GPU (concurrent streams or threads)
- * race; calls ordered on a stream do not.  Results equal lc_attn_decode's. */
+ * race; calls ordered on a stream do not.  The array used is that of the
+ * stream's device (the current device for a null stream).  Results equal
+ * lc_attn_decode's. */
 #define LC_DECODE_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
 int lc_attn_decode_static(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask,
                           const void* q, const void* k, const void* v, float* o, float* m,
@@ -165,11 +167,18 @@ int lc_attn_bwd_shard(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, 
  * dq_acc, dk_acc and dv_acc all set, d = 128 on the bf16 MFMA path and a
  * 256-byte-aligned workspace, the dK/dV kernel stores dS (bf16) in the
  * workspace and dQ is computed from it, without recomputing the scores.  The
- * workspace holds the dS of a chunk of query rows at a time: the full size
- * from lc_attn_bwd_shard_workspace_bytes runs the pair in chunks of up to
- * 65,536 rows; a smaller one runs smaller chunks (multiples of 256 rows).
- * With no usable workspace, or other shapes, this is lc_attn_bwd_shard.
- * Results agree with lc_attn_bwd_shard up to fp32 summation order. */
+ * workspace holds the dS of a chunk of query rows at a time (2 bytes per
+ * query row, key and query head): lc_attn_bwd_shard_workspace_bytes returns
+ * the size for chunks of min(q_tokens, 65,536) rows, or, when that exceeds
+ * LC_BWD_DS_WORKSPACE_CAP (32 GiB, the full size at 32,768 x 32,768 tokens
+ * and 16 heads), the size for the largest multiple of 256 rows within the
+ * cap, and 0 when not even 256 rows fit (very long KV shards: the
+ * recomputing kernels then run, as without a workspace).  A smaller
+ * workspace runs smaller chunks (multiples of 256 rows); every chunk streams
+ * the whole KV shard and updates dK/dV once more.  With no usable
+ * workspace, or other shapes, this is lc_attn_bwd_shard.  Results agree with
+ * lc_attn_bwd_shard up to fp32 summation order. */
+#define LC_BWD_DS_WORKSPACE_CAP ((size_t)32 << 30)
 size_t lc_attn_bwd_shard_workspace_bytes(const lc_attn_shape_t* shape);
 int lc_attn_bwd_shard_ws(const lc_attn_shape_t* shape, const lc_attn_mask_t* mask, const void* q,
                          const void* k, const void* v, const void* dout, const float* lse2,
@@ -198,6 +207,16 @@ typedef struct lc_ring_desc {
 
 size_t lc_ring_fwd_workspace_bytes(const lc_ring_desc_t* desc);
 size_t lc_ring_bwd_workspace_bytes(const lc_ring_desc_t* desc);
+/* Workspace for lc_ring_bwd that also holds the dS of the diagonal pair
+ * (this rank's queries against its own keys, hop 0 of both of the
+ * reference's passes, rs:367-416 and rs:418-460): lc_ring_bwd_workspace_bytes
+ * plus lc_attn_bwd_shard_workspace_bytes of that pair, when the pair takes
+ * the d = 128 bf16 MFMA path and q_position_start is None (or rank *
+ * local_tokens, so both passes see the pair at the same positions);
+ * otherwise the same as lc_ring_bwd_workspace_bytes.  At world = 1 (the
+ * dense attention of model.rs:223-252) the diagonal pair is the whole
+ * backward. */
+size_t lc_ring_bwd_ds_workspace_bytes(const lc_ring_desc_t* desc);
 
 /* ring_causal_attention_forward_with_stats (ring_attention.rs:139-233) on
  * device pointers: qs/ks/vs hold `world` shard pointers in rank order; hop h
@@ -213,7 +232,12 @@ int lc_ring_fwd_with_stats(const lc_ring_desc_t* desc, const void* const* qs,
  * statistics and upstream gradient.  Returns this rank's dq [B,n,Hq,D] and
  * dk, dv [B,n,Hkv,D] in dtype.  Pass 1 uses query positions owner*n + i and
  * pass 2 uses q_position_start (default rank*n) + i, as the reference does
- * (rs:377, rs:419). */
+ * (rs:377, rs:419).  The workspace needs lc_ring_bwd_workspace_bytes; with
+ * more (up to lc_ring_bwd_ds_workspace_bytes), the diagonal pair's dK/dV and
+ * dQ come from one dS-sharing run (the dK/dV kernel stores dS in the extra
+ * bytes, the dQ kernel reads it) instead of a recomputing run of each, with
+ * the same results up to fp32 summation order.  The host form below uses
+ * the larger workspace when it can allocate it. */
 int lc_ring_bwd(const lc_ring_desc_t* desc, const void* const* qs, const void* const* ks,
                 const void* const* vs, const void* const* outs, const float* const* ms,
                 const float* const* ls, const void* const* grad_outs, void* dq, void* dk,

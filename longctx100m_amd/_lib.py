@@ -129,6 +129,7 @@ SIGNATURES = {
                                      c_void_p]),
     "lc_ring_fwd_workspace_bytes": (c_size_t, [_R]),
     "lc_ring_bwd_workspace_bytes": (c_size_t, [_R]),
+    "lc_ring_bwd_ds_workspace_bytes": (c_size_t, [_R]),
     "lc_ring_fwd_with_stats": (c_int, [_R, _vpp, _vpp, _vpp, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_size_t, c_void_p]),
     "lc_ring_bwd": (c_int, [_R, _vpp, _vpp, _vpp, _vpp, _vpp, _vpp, _vpp, c_void_p, c_void_p,

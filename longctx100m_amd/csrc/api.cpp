@@ -59,6 +59,10 @@ size_t dtype_size(int dtype) { return dtype == LC_DTYPE_BF16 ? 2 : 4; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Checks common to every shape: mirrors the reference's shape errors.
+// Every flag bit this library defines; any other bit is rejected, so that a
+// stray or uninitialised flags word cannot select a mode by accident.
+constexpr uint32_t kKnownFlags = LC_FLAG_PRECISE | LC_FLAG_ACCUMULATE;
+
 int check_shape(const lc_attn_shape_t* s) {
   if (s == nullptr) return set_error(LC_ERR_INVALID, "null shape argument");
   if (s->batch <= 0 || s->heads_q <= 0 || s->heads_kv <= 0 || s->head_dim <= 0 ||
@@ -71,6 +75,8 @@ int check_shape(const lc_attn_shape_t* s) {
     return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", s->dtype);
   if (s->head_dim > 256)
     return set_error(LC_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", s->head_dim);
+  if (s->flags & ~kKnownFlags)
+    return set_error(LC_ERR_INVALID, "unknown flag bits 0x%x", s->flags & ~kKnownFlags);
   return LC_OK;
 }
 
@@ -212,14 +218,19 @@ int64_t ds_chunk_rows(const lc::Problem& p, size_t ws_bytes) {
   int64_t rows = (int64_t)(ws_bytes / per_tile) * 32;
   rows = std::min<int64_t>(rows, kStreamChunk);
   rows = rows >= p.Nq ? p.Nq : rows / 256 * 256;
-  // block indices of one chunk are 32-bit in the kernels
-  if ((int64_t)p.B * p.Hq * ((rows + 31) / 32) * nkb >= (int64_t)1 << 31) return 0;
   return rows;
 }
 
+// The dS of min(Nq, kStreamChunk) query rows, or, when that exceeds
+// LC_BWD_DS_WORKSPACE_CAP, of the largest multiple of 256 rows within the cap
+// (0 when not even 256 rows fit: such shards run the recomputing kernels).
 size_t ds_workspace_bytes(const lc::Problem& p) {
+  const size_t per_tile = (size_t)p.B * p.Hq * ((p.Nk + 31) / 32) * lc::kDsBlockBytes;
   const int64_t rows = std::min<int64_t>(p.Nq, kStreamChunk);
-  return (size_t)p.B * p.Hq * ((rows + 31) / 32) * ((p.Nk + 31) / 32) * lc::kDsBlockBytes;
+  const size_t full = per_tile * (size_t)((rows + 31) / 32);
+  if (full <= LC_BWD_DS_WORKSPACE_CAP) return full;
+  const size_t capped_rows = LC_BWD_DS_WORKSPACE_CAP / per_tile * 32 / 256 * 256;
+  return capped_rows == 0 ? 0 : per_tile * (capped_rows / 32);
 }
 
 bool ds_path(const lc::Problem& p, const void* q, const void* k, const void* v, const void* dout) {
@@ -281,6 +292,8 @@ int check_ring(const lc_ring_desc_t* d) {
     return set_error(LC_ERR_UNSUPPORTED, "unsupported dtype %d", d->dtype);
   if (d->head_dim > 256)
     return set_error(LC_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", d->head_dim);
+  if (d->flags & ~kKnownFlags)
+    return set_error(LC_ERR_INVALID, "unknown flag bits 0x%x", d->flags & ~kKnownFlags);
   if (d->flags & LC_FLAG_ACCUMULATE)
     return set_error(LC_ERR_INVALID, "LC_FLAG_ACCUMULATE applies to lc_attn_fwd_shard only");
   return LC_OK;
@@ -414,7 +427,7 @@ int lc_attn_decode_static(const lc_attn_shape_t* shape, const lc_attn_mask_t* ma
                      "use lc_attn_decode with a workspace",
                      need, lc::kDecodeStaticScratchBytes);
   void* scratch = nullptr;
-  LC_TRY_HIP(lc::decode_static_scratch(&scratch), "lc_attn_decode_static scratch address");
+  LC_TRY_HIP(lc::decode_static_scratch(st, &scratch), "lc_attn_decode_static scratch address");
   hipError_t e = lc::launch_decode128(p, q, k, v, o, m, l, scratch, st);
   return e == hipSuccess ? LC_OK : hip_error(e, "lc_attn_decode_static launch");
 }
@@ -526,6 +539,16 @@ size_t lc_ring_bwd_workspace_bytes(const lc_ring_desc_t* desc) {
   return bwd_ws_bytes(desc);
 }
 
+size_t lc_ring_bwd_ds_workspace_bytes(const lc_ring_desc_t* desc) {
+  if (check_ring(desc) != LC_OK) return 0;
+  const size_t base = bwd_ws_bytes(desc);
+  const int64_t rn = (int64_t)desc->rank * desc->local_tokens;
+  const int64_t q_pos0 = desc->q_position_start >= 0 ? desc->q_position_start : rn;
+  const lc::Problem pd = ring_problem(desc, rn, rn);
+  if (q_pos0 != rn || !pair_active(pd) || pd.D != 128 || !lc::mfma_supported(pd)) return base;
+  return base + ds_workspace_bytes(pd);
+}
+
 int lc_ring_fwd_with_stats(const lc_ring_desc_t* d, const void* const* qs, const void* const* ks,
                            const void* const* vs, void* out, float* m, float* l, void* workspace,
                            size_t workspace_bytes, void* stream) {
@@ -606,12 +629,38 @@ int lc_ring_bwd(const lc_ring_desc_t* d, const void* const* qs, const void* cons
   LC_TRY_HIP(lc::launch_fill_zero(dk_acc, (int64_t)n_k, st), "lc_ring_bwd zero");
   LC_TRY_HIP(lc::launch_fill_zero(dv_acc, (int64_t)n_k, st), "lc_ring_bwd zero");
 
+  // The diagonal pair (this rank's queries against this rank's keys) is hop 0
+  // of both passes: pass 1 takes its dK/dV, pass 2 its dQ, with the same
+  // positions when q_position_start is the default.  Given workspace beyond
+  // bwd_ws_bytes, both come from one dS-sharing run of that pair (the dK/dV
+  // kernel stores dS, dQ is formed from it) instead of two recomputing runs.
+  const int64_t q_pos0 = d->q_position_start >= 0 ? d->q_position_start : (int64_t)r * n;
+  const lc::Problem pd = ring_problem(d, (int64_t)r * n, (int64_t)r * n);
+  int64_t ds_chunk = 0;
+  uint16_t* ds = nullptr;
+  if (q_pos0 == (int64_t)r * n && pair_active(pd) &&
+      ds_path(pd, qs[r], ks[r], vs[r], grad_outs[r]) && workspace_bytes > bwd_ws_bytes(d)) {
+    ds = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + bwd_ws_bytes(d));
+    ds_chunk = ds_chunk_rows(pd, workspace_bytes - bwd_ws_bytes(d));
+  }
+  if (ds_chunk > 0) {
+    LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[r],
+                                         grad_outs[r], ms[r], ls[r], delta, lse2, st),
+               "lc_ring_bwd preprocess");
+    if (int rc = bwd_shard_ds(pd, ds_chunk, qs[r], ks[r], vs[r], grad_outs[r], lse2, delta,
+                              dq_acc, dk_acc, dv_acc, ds, st))
+      return rc;
+  }
+
   // Pass 1 (rs:367-416): local KV fixed, query owners rank, rank-1, ...;
   // query positions owner*n + i.
+  bool pass1_stats = false;  // delta / lse2 hold another owner's statistics
   for (int hop = 0; hop < d->world; ++hop) {
     const int qo = ((r - hop) % d->world + d->world) % d->world;
+    if (qo == r && ds_chunk > 0) continue;  // done above
     const lc::Problem p = ring_problem(d, (int64_t)qo * n, (int64_t)r * n);
     if (!pair_active(p)) continue;
+    pass1_stats = true;
     LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[qo],
                                          grad_outs[qo], ms[qo], ls[qo], delta, lse2, st),
                "lc_ring_bwd preprocess");
@@ -622,12 +671,13 @@ int lc_ring_bwd(const lc_ring_desc_t* d, const void* const* qs, const void* cons
 
   // Pass 2 (rs:418-460): local Q fixed with positions q_position_start
   // (default rank*n) + i, KV owners rank, rank-1, ...
-  const int64_t q_pos0 = d->q_position_start >= 0 ? d->q_position_start : (int64_t)r * n;
-  LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[r],
-                                       grad_outs[r], ms[r], ls[r], delta, lse2, st),
-             "lc_ring_bwd preprocess");
+  if (ds_chunk == 0 || pass1_stats)
+    LC_TRY_HIP(lc::launch_bwd_preprocess(d->batch, n, d->heads_q, d->head_dim, d->dtype, outs[r],
+                                         grad_outs[r], ms[r], ls[r], delta, lse2, st),
+               "lc_ring_bwd preprocess");
   for (int hop = 0; hop < d->world; ++hop) {
     const int owner = ((r - hop) % d->world + d->world) % d->world;
+    if (owner == r && ds_chunk > 0) continue;  // done above
     const lc::Problem p = ring_problem(d, q_pos0, (int64_t)owner * n);
     if (!pair_active(p)) continue;
     if (int rc = bwd_shard(p, qs[r], ks[owner], vs[owner], grad_outs[r], lse2, delta, dq_acc,
@@ -722,11 +772,19 @@ int lc_ring_bwd_host(const lc_ring_desc_t* d, const void* const* qs, const void*
     p_l[i] = static_cast<const float*>(bufs[7 * i + 6].p);
   }
   DevBuf dqb, dkb, dvb, wb;
-  const size_t ws = bwd_ws_bytes(d);
   LC_TRY_HIP(dqb.alloc(q_bytes), "hipMalloc");
   LC_TRY_HIP(dkb.alloc(kv_bytes), "hipMalloc");
   LC_TRY_HIP(dvb.alloc(kv_bytes), "hipMalloc");
-  LC_TRY_HIP(wb.alloc(ws), "hipMalloc");
+  // With room for the diagonal pair's dS the backward shares it between the
+  // dK/dV and dQ kernels; when that allocation fails, the base workspace
+  // runs the recomputing kernels instead.
+  size_t ws = lc_ring_bwd_ds_workspace_bytes(d);
+  if (ws > bwd_ws_bytes(d) && wb.alloc(ws) != hipSuccess) {
+    (void)hipGetLastError();  // the failed allocation's status; nothing was allocated
+    wb.p = nullptr;
+    ws = bwd_ws_bytes(d);
+  }
+  if (wb.p == nullptr) LC_TRY_HIP(wb.alloc(ws), "hipMalloc");
   if (int rc = lc_ring_bwd(d, p_q.data(), p_k.data(), p_v.data(), p_o.data(), p_m.data(),
                            p_l.data(), p_g.data(), dqb.p, dkb.p, dvb.p, wb.p, ws, nullptr))
     return rc;

@@ -683,8 +683,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
   // not include the stores (vector memory operations complete in issue order,
   // and the stores take longer): they have two steps to complete.
   bool stored = false;  // this step's top issued the two dS stores (after its loads)
-  int pend = -1;        // exchange block of ds_keep, not yet stored
-  auto store_ds = [&](int blkid) {
+  int64_t pend = -1;    // exchange block of ds_keep, not yet stored
+  auto store_ds = [&](int64_t blkid) {
     const int dsl = ds_slot(opaque(kc), opaque(h));
     typedef __attribute__((address_space(1))) bf16x8 gbl_bf16x8;  // global, not flat
     uint8_t* blk = reinterpret_cast<uint8_t*>(a.ds + (int64_t)blkid * kDsBlockElems);
@@ -720,8 +720,8 @@ __global__ __launch_bounds__(256, 2) void dkdv128_kernel(Bwd128Args a) {
     if (kw0 >= a.Nk) continue;
     if (a.causal && wk_first > qp_last) continue;
     const int buf = step & 1;
-    const int dsblk = a.ds == nullptr ? -1
-        : ((b * a.Hq + hq_c) * a.ds_nqt + qrow0 / kKvBM) * a.ds_nkb + kw0 / kKvKW;
+    const int64_t dsblk = a.ds == nullptr ? -1
+        : (((int64_t)b * a.Hq + hq_c) * a.ds_nqt + qrow0 / kKvBM) * a.ds_nkb + kw0 / kKvKW;
     pend = dsblk;
     if ((a.causal && wk_last > qp_first) || wk_last >= a.valid || kw0 + kKvKW > a.Nk ||
         qrow0 + kKvBM > a.Nq) {

@@ -335,18 +335,34 @@ size_t decode_workspace_bytes(const Problem& p) {
   return (size_t)(S * rows * D * 4 + 2 * S * rows * 4);
 }
 
-hipError_t decode_static_scratch(void** ptr) {
+hipError_t decode_static_scratch(hipStream_t st, void** ptr) {
   constexpr int kMaxDevices = 64;
   static std::mutex mu;
   static void* addr[kMaxDevices] = {};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  // The kernels run on the stream's device, so the array must be that
+  // device's copy: a null stream means the current device.
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return e;
+  int dev = cur;
+  if (st != nullptr) {
+    hipDevice_t sd = 0;
+    e = hipStreamGetDevice(st, &sd);
+    if (e != hipSuccess) return e;
+    dev = (int)sd;
+  }
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(mu);
   if (addr[dev] == nullptr) {
+    // hipGetSymbolAddress resolves the symbol on the current device: make
+    // the stream's device current for the lookup, then restore the caller's.
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with `dev` current
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
     if (e != hipSuccess) return e;
     addr[dev] = p;
   }

@@ -368,7 +368,10 @@ __global__ __launch_bounds__(64 * kSplit) void gemv_fused_kernel(GemvFused a) {
     __syncthreads();  // part is rewritten by the next block
   };
 
-  if (IN == kInNorm || ce - cb <= 64 * kFusedUnroll) {  // the norm form has cols <= 4096
+  // The choice depends on `per` (the same for every wave), not on the wave's
+  // own ce - cb (shorter for the last wave), so all waves of the workgroup
+  // take the same loop and reach finish()'s barriers from the same place.
+  if (IN == kInNorm || per <= 64 * kFusedUnroll) {  // the norm form has cols <= 4096
     // One round per row (rows of up to 4096 columns, so every folded-norm
     // call): the lane's chunks of the multiplied vector are formed once and
     // kept in registers, and the next block's weight loads are issued before

@@ -104,9 +104,10 @@ hipError_t launch_decode128(const Problem& p, const void* q, const void* k, cons
                             float* o, float* m, float* l, void* ws, hipStream_t s);
 // Bytes of decode.hip's file-scope device array that stands in for the
 // workspace of lc_attn_decode_static, and that array's address on the
-// current device (looked up once per device; allocates nothing).
+// device of stream st (the current device for a null stream; looked up once
+// per device; allocates nothing).
 constexpr size_t kDecodeStaticScratchBytes = size_t(16) << 20;
-hipError_t decode_static_scratch(void** ptr);
+hipError_t decode_static_scratch(hipStream_t st, void** ptr);
 
 // Decoder-layer row kernels (layer.hip).
 hipError_t launch_rmsnorm(int dtype, int64_t rows, int cols, float eps, const void* x,

@@ -236,6 +236,33 @@ int lc_gemv_fused(const lc_gemv_fused_t* f, int64_t rows, int32_t cols, const vo
     default:
       return set_error(LC_ERR_INVALID, "unknown gemv output form %d", f->out_form);
   }
+  {
+    // Every workgroup reads x, residual and residual_out's sources while
+    // others write their output rows, so no output may share bytes with them.
+    struct Range {
+      uintptr_t lo, hi;
+    };
+    auto range = [](const void* p, size_t bytes) {
+      const auto b = reinterpret_cast<uintptr_t>(p);
+      return Range{b, p ? b + bytes : b};
+    };
+    auto meet = [](Range a, Range b) { return a.lo < b.hi && b.lo < a.hi; };
+    const size_t xb = (size_t)cols * (f->in_form == LC_GEMV_IN_F32 ? 4 : 2);
+    const Range ins[3] = {range(x, xb), range(f->residual, 2 * (size_t)cols),
+                          range(f->residual_out, 2 * (size_t)cols)};
+    size_t yn = (size_t)rows;  // bf16 elements of y
+    if (f->out_form == LC_GEMV_OUT_SWIGLU) yn = (size_t)rows / 2;
+    if (f->out_form == LC_GEMV_OUT_ROPE_QKV) yn = (size_t)f->q_heads * f->head_dim;
+    const size_t kvn = (size_t)f->kv_heads * f->head_dim;
+    const bool rope = f->out_form == LC_GEMV_OUT_ROPE_QKV;
+    const Range outs[3] = {range(y, 2 * yn), range(rope ? f->k_out : nullptr, 2 * kvn),
+                           range(rope ? f->v_out : nullptr, 2 * kvn)};
+    for (const Range& o : outs)
+      for (const Range& i : ins)
+        if (meet(o, i))
+          return set_error(LC_ERR_INVALID,
+                           "gemv outputs must not overlap x, residual or residual_out");
+  }
   if (rows == 0) return LC_OK;
   hipError_t e = lc::launch_gemv_fused(
       f->in_form, f->out_form, rows, cols, w, w_stride, x, y, f->residual, f->residual_out,

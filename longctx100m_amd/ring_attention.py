@@ -282,8 +282,13 @@ def ring_causal_attention_forward(shards, rank, causal=True, block_q=64, block_k
 
 def ring_causal_attention_backward(shards, rank, outs, ms, ls, grad_outs, causal=True,
                                    block_q=64, block_k=128, valid_length=None,
-                                   q_position_start=None, *, precise=False):
-    """(dq [B,n,Hq,D], dk [B,n,Hkv,D], dv [B,n,Hkv,D]) of rank ``rank``'s shard."""
+                                   q_position_start=None, *, precise=False, share_ds=True):
+    """(dq [B,n,Hq,D], dk [B,n,Hkv,D], dv [B,n,Hkv,D]) of rank ``rank``'s shard.
+
+    ``share_ds``: give lc_ring_bwd the workspace of lc_ring_bwd_ds_workspace_bytes,
+    so that the diagonal pair (hop 0 of both passes; the whole backward at
+    world 1) runs its dK/dV and dQ kernels on one shared dS instead of
+    recomputing the scores twice."""
     desc = _ring_desc(shards, rank, causal, block_q, block_k, valid_length, q_position_start,
                       precise)
     world = len(shards)
@@ -302,7 +307,8 @@ def ring_causal_attention_backward(shards, rank, outs, ms, ls, grad_outs, causal
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(k)
-    ws_bytes = lib.lc_ring_bwd_workspace_bytes(desc)
+    ws_bytes = (lib.lc_ring_bwd_ds_workspace_bytes(desc) if share_ds
+                else lib.lc_ring_bwd_workspace_bytes(desc))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     arrs = [_lib.ptr_array([t.data_ptr() for t in ts]) for ts in
             ([s[0] for s in shards], [s[1] for s in shards], [s[2] for s in shards], outs, ms,

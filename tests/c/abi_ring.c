@@ -12,6 +12,14 @@
  *                       against the C restatement oracle/ring_ref.c (test
  *                       infrastructure, linked here only as the checker) at
  *                       the fp32 bar of 1e-5 norm-relative
+ *   abi_ring customop3  the exact call sequence of the candle CustomOp3 that
+ *                       replaces the dense attention of model.rs:223-252
+ *                       (longctx100m_amd/rust/amd_attn.rs): one rank, GQA
+ *                       (Hq 8 / Hkv 2), d 128, bf16 host buffers of 700
+ *                       tokens; cpu_fwd = lc_ring_fwd_with_stats_host keeping
+ *                       m and l, bwd = lc_ring_bwd_host with the op's output,
+ *                       the saved m and l and a bf16 upstream gradient; checked
+ *                       against the C restatement at the bf16 bar of 2e-2
  *
  * Prints one line per check and "abi_ring: ok" at the end; exit status 0 on
  * success.
@@ -221,6 +229,112 @@ static int config1(void) {
   return 0;
 }
 
+/* bf16 <-> fp32: round to nearest even, as torch and candle's half crate do */
+static uint16_t to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+static float from_bf16(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+/* N(0,1) values rounded to bf16: the bits for the library, the values for the oracle */
+static void fill_bf16(uint16_t* bits, float* vals, size_t n) {
+  fill_normal(vals, n);
+  for (size_t i = 0; i < n; ++i) {
+    bits[i] = to_bf16(vals[i]);
+    vals[i] = from_bf16(bits[i]);
+  }
+}
+
+static int customop3(void) {
+  enum { T = 700, HQ = 8, HKV = 2, D = 128, G = HQ / HKV };
+  const size_t nq = (size_t)T * HQ * D, nk = (size_t)T * HKV * D, ns = (size_t)HQ * T;
+  uint16_t *qb = malloc(nq * 2), *kb = malloc(nk * 2), *vb = malloc(nk * 2), *gb = malloc(nq * 2);
+  float *qf = malloc(nq * 4), *kf = malloc(nk * 4), *vf = malloc(nk * 4), *gf = malloc(nq * 4);
+  sm_state = 20260723u;
+  fill_bf16(qb, qf, nq);
+  fill_bf16(kb, kf, nk);
+  fill_bf16(vb, vf, nk);
+  fill_bf16(gb, gf, nq);
+  /* CausalAttention::cpu_fwd: desc(1, 0, dims, hkv, bf16, causal, 64, 128, None, None) */
+  lc_ring_desc_t d = desc(1, 0, T, HQ, HKV, D);
+  d.dtype = LC_DTYPE_BF16;
+  uint16_t* out = malloc(nq * 2);
+  float *m = malloc(ns * 4), *l = malloc(ns * 4);
+  const void* pq[1] = {qb};
+  const void* pk[1] = {kb};
+  const void* pv[1] = {vb};
+  int rc = lc_ring_fwd_with_stats_host(&d, pq, pk, pv, out, m, l);
+  if (rc) {
+    printf("FAIL: cpu_fwd lc_ring_fwd_with_stats_host: %s\n", lc_last_error());
+    return 1;
+  }
+  /* CausalAttention::bwd: ring_causal_attention_backward(&[(q, k, v)], 0, &[res], &[m], &[l],
+   * &[grad]) -> lc_ring_bwd_host with the op's own output and the saved statistics */
+  uint16_t *dqb = malloc(nq * 2), *dkb = malloc(nk * 2), *dvb = malloc(nk * 2);
+  const void* po[1] = {out};
+  const float* pm[1] = {m};
+  const float* pl[1] = {l};
+  const void* pg[1] = {gb};
+  rc = lc_ring_bwd_host(&d, pq, pk, pv, po, pm, pl, pg, dqb, dkb, dvb);
+  if (rc) {
+    printf("FAIL: bwd lc_ring_bwd_host: %s\n", lc_last_error());
+    return 1;
+  }
+  /* the oracle on the same bf16 values, KV heads expanded (model.rs:85-94) */
+  float* ke = expand_heads(kf, T, HKV, G, D);
+  float* ve = expand_heads(vf, T, HKV, G, D);
+  float *rout = malloc(nq * 4), *rm = malloc(ns * 4), *rl = malloc(ns * 4);
+  const float* oq[1] = {qf};
+  const float* ok[1] = {ke};
+  const float* ov[1] = {ve};
+  if (ref_ring_fwd_with_stats(1, 0, 1, T, HQ, D, oq, ok, ov, 1, 64, 128, -1, -1, rout, rm, rl)) {
+    printf("FAIL: oracle forward\n");
+    return 1;
+  }
+  float* outf = malloc(nq * 4);
+  for (size_t i = 0; i < nq; ++i) outf[i] = from_bf16(out[i]);
+  char what[160];
+  const double eo = norm_rel(outf, rout, nq), el = norm_rel(l, rl, ns), em = norm_rel(m, rm, ns);
+  snprintf(what, sizeof what, "customop3 fwd out %.2e <= 2e-2, m %.2e l %.2e <= 1e-4", eo, em, el);
+  check(eo <= 2e-2 && em <= 1e-4 && el <= 1e-4, what);
+  /* the backward's delta uses the forward output in the input dtype (py:314) */
+  float* routb = malloc(nq * 4);
+  for (size_t i = 0; i < nq; ++i) routb[i] = from_bf16(to_bf16(rout[i]));
+  float *rdq = malloc(nq * 4), *rdk = malloc(nq * 4), *rdv = malloc(nq * 4);
+  const float* oo[1] = {routb};
+  const float* om[1] = {rm};
+  const float* ol[1] = {rl};
+  const float* og[1] = {gf};
+  if (ref_ring_bwd(1, 0, 1, T, HQ, D, oq, ok, ov, oo, om, ol, og, 1, 64, 128, -1, -1, rdq, rdk,
+                   rdv)) {
+    printf("FAIL: oracle backward\n");
+    return 1;
+  }
+  float *sdk = calloc(nk, 4), *sdv = calloc(nk, 4);
+  for (int t = 0; t < T; ++t)
+    for (int h = 0; h < HQ; ++h)
+      for (int j = 0; j < D; ++j) {
+        sdk[((size_t)t * HKV + h / G) * D + j] += rdk[((size_t)t * HQ + h) * D + j];
+        sdv[((size_t)t * HKV + h / G) * D + j] += rdv[((size_t)t * HQ + h) * D + j];
+      }
+  float *dqf = malloc(nq * 4), *dkf = malloc(nk * 4), *dvf = malloc(nk * 4);
+  for (size_t i = 0; i < nq; ++i) dqf[i] = from_bf16(dqb[i]);
+  for (size_t i = 0; i < nk; ++i) {
+    dkf[i] = from_bf16(dkb[i]);
+    dvf[i] = from_bf16(dvb[i]);
+  }
+  const double eq = norm_rel(dqf, rdq, nq), ek = norm_rel(dkf, sdk, nk), ev = norm_rel(dvf, sdv, nk);
+  snprintf(what, sizeof what, "customop3 bwd dq %.2e dk %.2e dv %.2e <= 2e-2", eq, ek, ev);
+  check(eq <= 2e-2 && ek <= 2e-2 && ev <= 2e-2, what);
+  return 0;
+}
+
 int main(int argc, char** argv) {
   const char* mode = argc > 1 ? argv[1] : "validate";
   int rc = 0;
@@ -228,8 +342,10 @@ int main(int argc, char** argv) {
     rc = validate();
   else if (strcmp(mode, "config1") == 0)
     rc = config1();
+  else if (strcmp(mode, "customop3") == 0)
+    rc = customop3();
   else {
-    fprintf(stderr, "usage: abi_ring validate|config1\n");
+    fprintf(stderr, "usage: abi_ring validate|config1|customop3\n");
     return 2;
   }
   if (rc || failures) {

@@ -68,6 +68,8 @@ def _desc(**kw):
     (dict(head_dim=0), _lib.LC_ERR_INVALID,
      "q, k, v must have shape [batch, tokens, heads, head_dim]"),
     (dict(dtype=7), _lib.LC_ERR_UNSUPPORTED, "unsupported dtype 7"),
+    (dict(flags=4), _lib.LC_ERR_INVALID, "unknown flag bits 0x4"),
+    (dict(flags=0x80000001), _lib.LC_ERR_INVALID, "unknown flag bits 0x80000000"),
 ])
 def test_ring_validation_messages(lib, kw, code, msg):
     d = _desc(**kw)
@@ -89,6 +91,22 @@ def test_workspace_sizes(lib):
     n_s = 16 * 32768
     assert lib.lc_ring_fwd_workspace_bytes(d) == 4 * n_o  # the running output; m, l are outputs
     assert lib.lc_ring_bwd_workspace_bytes(d) == 3 * 4 * n_o + 2 * 4 * n_s
+    # with room for the diagonal pair's dS: 32,768^2 keys x 16 heads x 2 bytes = the 32 GiB cap
+    base = lib.lc_ring_bwd_workspace_bytes(d)
+    assert lib.lc_ring_bwd_ds_workspace_bytes(d) == base + (32 << 30)
+    # no sharing: q_position_start away from rank * n, fp32, the fp32-math flag, d != 128
+    for kw in (dict(q_position_start=5), dict(dtype=_lib.LC_DTYPE_F32),
+               dict(flags=_lib.LC_FLAG_PRECISE), dict(head_dim=64)):
+        dd = _desc(**dict(dict(local_tokens=32768, heads_q=16, heads_kv=16, head_dim=128,
+                               world=8, rank=7), **kw))
+        assert lib.lc_ring_bwd_ds_workspace_bytes(dd) == lib.lc_ring_bwd_workspace_bytes(dd)
+    dd = _desc(local_tokens=32768, heads_q=16, heads_kv=16, head_dim=128, world=8, rank=7,
+               q_position_start=7 * 32768)  # the default position given explicitly
+    assert lib.lc_ring_bwd_ds_workspace_bytes(dd) == base + (32 << 30)
+    one = _desc(world=1, rank=0, local_tokens=100, heads_q=4, heads_kv=2, head_dim=128)
+    assert lib.lc_ring_bwd_ds_workspace_bytes(one) == \
+        lib.lc_ring_bwd_workspace_bytes(one) + 4 * 4 * 4 * 2048
+    assert lib.lc_ring_bwd_ds_workspace_bytes(_desc(rank=5)) == 0  # invalid descriptor
 
 
 def test_null_and_workspace_errors(lib):
@@ -132,6 +150,27 @@ def test_accumulate_flag_is_for_fwd_shard_only(lib):
     assert rc == _lib.LC_ERR_INVALID and lib.lc_last_error().decode() == msg
 
 
+def test_unknown_flag_bits_rejected(lib):
+    """A flags word with a bit this library does not define (a stray or
+    uninitialised value) is rejected before any device work by every entry
+    point that takes a shape, instead of selecting a mode by accident."""
+    shape = _lib.Shape(1, 4, 4, 2, 2, 64, _lib.LC_DTYPE_BF16, 4)
+    mask = _lib.Mask(0, 0, -1, 1, 0)
+    msg = "unknown flag bits 0x4"
+    assert lib.lc_attn_fwd_shard(shape, mask, 16, 16, 16, 16, 16, 16, None) == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == msg
+    assert lib.lc_attn_bwd_shard(shape, mask, 16, 16, 16, 16, 16, 16, 16, 16, 16,
+                                 None) == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == msg
+    assert lib.lc_attn_bwd_shard_workspace_bytes(shape) == 0
+    assert lib.lc_attn_decode_static(shape, mask, 16, 16, 16, 16, 16, 16,
+                                     None) == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == msg
+    shape.flags = _lib.LC_FLAG_PRECISE | _lib.LC_FLAG_ACCUMULATE | 8
+    assert lib.lc_attn_merge(shape, 16, 16, 16, 16, 16, 16, None, None) == _lib.LC_ERR_INVALID
+    assert lib.lc_last_error().decode() == "unknown flag bits 0x8"
+
+
 def test_last_error_is_per_thread(lib):
     import threading
 
@@ -159,6 +198,13 @@ def test_shared_ds_workspace_size_and_errors(lib):
     assert size(1, 32768, 32768, 16, 16, 128, bf, 0) == 16 * 1024 * 1024 * 2048
     assert size(2, 100, 70, 4, 2, 128, bf, 0) == 2 * 4 * 4 * 3 * 2048
     assert size(1, 200000, 64, 1, 1, 128, bf, 0) == 2048 * 2 * 2048  # 65,536-row chunks
+    # capped at 32 GiB: a 1M-key shard gets the largest multiple of 256 rows that fits
+    cap = 32 << 30
+    per32 = 16 * (1_000_000 // 32) * 2048  # one 32-row query tile, 16 heads
+    assert size(1, 1_000_000, 1_000_000, 16, 16, 128, bf, 0) == (cap // per32 * 32 // 256 * 256 // 32) * per32
+    assert size(1, 1_000_000, 1_000_000, 16, 16, 128, bf, 0) <= cap
+    assert size(1, 65536, 65536, 16, 16, 128, bf, 0) == cap  # 128 GiB for 65,536 rows: 16,384
+    assert size(1, 4096, 8_000_000, 16, 16, 128, bf, 0) == 0  # not even 256 rows fit
     assert size(1, 256, 256, 2, 2, 64, bf, 0) == 0
     assert size(1, 256, 256, 2, 2, 128, f32, 0) == 0
     assert size(1, 256, 256, 2, 2, 128, bf, _lib.LC_FLAG_PRECISE) == 0
@@ -191,7 +237,9 @@ def test_gemv_argument_errors(lib):
 def test_gemv_fused_argument_errors(lib):
     """lc_gemv_fused checks its forms before any launch.  Every call here fails
     a check or has rows = 0 (which returns after the checks), so none reaches
-    a launch with these placeholder pointers."""
+    a launch with these placeholder pointers.  Outputs (y, and k_out / v_out of
+    the rope form) that share a byte with x, residual or residual_out are
+    rejected: other workgroups still read those while one writes its rows."""
     G = _lib.GemvFused
 
     def call(f, rows=0, cols=64):
@@ -228,6 +276,32 @@ def test_gemv_fused_argument_errors(lib):
         "rope_row must be 4-byte and k_out, v_out 2-byte aligned"
     assert call(G(**dict(rope, v_out=17)), rows=64)[1] == \
         "rope_row must be 4-byte and k_out, v_out 2-byte aligned"
+
+    def call_xy(f, rows, cols, x, y):
+        rc = lib.lc_gemv_fused(ctypes.byref(f), rows, cols, 16, cols, x, y, None)
+        return rc, lib.lc_last_error().decode()
+
+    ovl = "gemv outputs must not overlap x, residual or residual_out"
+    # y (rows bf16) against x (cols bf16 / fp32): in place, or sharing a byte
+    assert call_xy(G(), 64, 64, 4096, 4096) == (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(), 64, 64, 4096, 4096 + 126) == (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(), 64, 64, 4096 + 16, 4096 + 16 - 126) == (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(in_form=_lib.LC_GEMV_IN_F32), 64, 64, 4096, 4096 + 254) == \
+        (_lib.LC_ERR_INVALID, ovl)
+    # the folded norm: y against residual and residual_out
+    nrm = dict(in_form=_lib.LC_GEMV_IN_RMSNORM, norm_weight=16, residual=8192,
+               residual_out=12288)
+    assert call_xy(G(**nrm), 64, 64, 4096, 8192 + 64) == (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(**nrm), 64, 64, 4096, 12288 - 64) == (_lib.LC_ERR_INVALID, ovl)
+    # swiglu writes rows / 2 elements; rope writes q_heads * head_dim, k_out, v_out
+    assert call_xy(G(out_form=_lib.LC_GEMV_OUT_SWIGLU), 128, 64, 4096, 4096 - 126) == \
+        (_lib.LC_ERR_INVALID, ovl)
+    rq = dict(rope, rope_row=16, k_out=20480, v_out=24576)
+    assert call_xy(G(**dict(rq, k_out=4096 + 64)), 64, 64, 4096, 16384) == \
+        (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(**dict(rq, v_out=4096 - 30)), 64, 64, 4096, 16384) == \
+        (_lib.LC_ERR_INVALID, ovl)
+    assert call_xy(G(**rq), 64, 64, 4096, 4096 - 62) == (_lib.LC_ERR_INVALID, ovl)
 
 
 def test_decode_workspace_checks(lib):

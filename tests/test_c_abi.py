@@ -1,7 +1,10 @@
 """The C ABI driven from C: tests/c/abi_ring.c binds include/longctx100m_attn.h
 as a non-Python caller would (plain pointers, the reference's host-pointer
-ring signatures) and checks validation texts (CPU) and BASELINE config 1's
-forward and backward of both ranks against the C oracle at 1e-5 (GPU)."""
+ring signatures) and checks validation texts (CPU), BASELINE config 1's
+forward and backward of both ranks against the C oracle at 1e-5 (GPU), and
+the call sequence of the candle CustomOp3 in longctx100m_amd/rust/amd_attn.rs
+(one rank, GQA, bf16 host buffers, the forward's saved m and l handed to the
+backward) against the C oracle at 2e-2 (GPU)."""
 
 import subprocess
 from pathlib import Path
@@ -37,3 +40,9 @@ def test_c_caller_validation(abi_ring):
 def test_c_caller_config1_against_c_oracle(abi_ring):
     out = _run(abi_ring, "config1", 120)
     assert out.count("pass: config 1 rank") == 6 and "FAIL" not in out
+
+
+@pytest.mark.gpu
+def test_c_caller_customop3_sequence_against_c_oracle(abi_ring):
+    out = _run(abi_ring, "customop3", 120)
+    assert out.count("pass: customop3") == 2 and "FAIL" not in out

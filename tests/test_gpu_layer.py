@@ -191,6 +191,87 @@ def test_layer_prefill_reduced(ly, gpu):
     assert norm_rel(_np(mlp), mlpw) <= 2e-2
 
 
+def test_layer_prefill_c4_shape(ly, gpu):
+    """Config 4's decoder layer at its own shape (model.rs:387-393): hidden 4096,
+    GQA 32/8, d 128, SwiGLU 14336, RoPE theta 5e5, bf16 weights N(0, 0.02), rank 3
+    of a 4-rank ring with 65,536 tokens per shard, so every query attends the 3
+    preceding KV shards and its own shard's keys up to it (196,609-262,144 keys).
+    The GPU computes the whole layer; 14 rows (shard ends, tile and wave
+    boundaries, random) are recomputed by the oracle composition in float64:
+    RMSNorm with the residual add, the projections on the bf16 operands rounded to
+    bf16, RoPE, attention of the row over every visible key, the output projection,
+    the second RMSNorm, SwiGLU and the down projection.  The oracle's K and V rows
+    of this shard (every one a sampled query sees) come from the oracle RMSNorm and
+    RoPE with the K/V projection as a float32 GEMM (torch) rounded to bf16; those
+    rows are checked against the float64 projection at the sampled rows."""
+    import torch
+
+    cfg = ly.C4
+    T, rank, d, hq, hkv = 65536, 3, cfg.head_dim, cfg.num_heads, cfg.num_key_value_heads
+    c, inter = cfg.hidden_size, cfg.intermediate_size
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(404)
+    w = ly.init_layer_weights(cfg, gen, "cuda")
+    w["norm1"] = (1 + 0.1 * torch.randn(c, generator=gen, device="cuda")).to(torch.bfloat16)
+    w["norm2"] = (1 + 0.1 * torch.randn(c, generator=gen, device="cuda")).to(torch.bfloat16)
+    x = torch.randn(T, c, generator=gen, device="cuda").to(torch.bfloat16)
+    res = (0.5 * torch.randn(T, c, generator=gen, device="cuda")).to(torch.bfloat16)
+    pre = [tuple((1.3 * torch.randn(1, T, hkv, d, generator=gen, device="cuda")).to(torch.bfloat16)
+                 for _ in range(2)) for _ in range(rank)]
+    table = ly.rope_table(ly.rope_params(d, cfg.rope_theta), T, rank * T)
+    x2, mlp = ly.layer_prefill(x, w, cfg, table, rank, pre, residual=res)
+    gpu.cuda.synchronize()
+    rows = np.array([0, 1, 31, 32, 255, 256, 4095, 4096, 32767, 32768, 50001, 65279, 65534,
+                     65535])
+    got_x2, got_mlp = _np(x2[rows]), _np(mlp[rows])
+    del x2, mlp
+
+    # oracle: first RMSNorm of every row (its K/V rows are visible to later queries)
+    W = {k: _np(v) for k, v in w.items()}
+    h_all, xin_all = L.rmsnorm(_np(x), W["norm1"], cfg.rms_norm_eps, residual=_np(res))
+    hb = torch.tensor(h_all, device="cuda")
+    wkv = w["wqkv"][hq * d:].float()
+    kvp = L.bf16(_np(hb @ wkv.t()))  # [T, 2 * hkv * d], float32 GEMM of the bf16 operands
+    del hb, wkv
+    gtab = _np(table)
+    k_loc = L.rope_apply(kvp[:, :hkv * d].reshape(T, hkv, d), gtab)
+    v_loc = kvp[:, hkv * d:].reshape(T, hkv, d)
+    del kvp
+
+    def gemm(a, b):  # a @ b.T on the bf16 operands in float64, rounded to bf16
+        return L.bf16(a.astype(np.float64) @ b.astype(np.float64).T)
+
+    h_r = h_all[rows]
+    qkv = gemm(h_r, W["wqkv"])
+    q = L.rope_apply(qkv[:, :hq * d].reshape(len(rows), hq, d), gtab[rows])
+    k_chk = L.rope_apply(qkv[:, hq * d:(hq + hkv) * d].reshape(len(rows), hkv, d), gtab[rows])
+    # the float32-GEMM K/V rows equal the float64 ones up to a bf16 rounding step
+    assert np.abs(k_chk - k_loc[rows]).max() <= 2 * BF16_ULP * np.abs(k_chk).max()
+    assert np.abs(qkv[:, (hq + hkv) * d:].reshape(len(rows), hkv, d) - v_loc[rows]).max() <= \
+        2 * BF16_ULP * np.abs(v_loc[rows]).max()
+    n_pre = rank * T
+    g = hq // hkv
+    scale = 1.0 / np.sqrt(d)
+    att = np.zeros((len(rows), hq, d))
+    for kh in range(hkv):
+        K = np.concatenate([_np(p[0][0, :, kh]) for p in pre] + [k_loc[:, kh]]).astype(np.float64)
+        V = np.concatenate([_np(p[1][0, :, kh]) for p in pre] + [v_loc[:, kh]]).astype(np.float64)
+        Q = q[:, kh * g:(kh + 1) * g].astype(np.float64).reshape(-1, d)  # [rows * g, d]
+        s = (Q @ K.T) * scale
+        vis = np.arange(K.shape[0])[None, :] <= (n_pre + np.repeat(rows, g))[:, None]
+        s = np.where(vis, s, -np.inf)
+        s -= s.max(1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(1, keepdims=True)
+        att[:, kh * g:(kh + 1) * g] = (p @ V).reshape(len(rows), g, d)
+    o = gemm(L.bf16(att).reshape(len(rows), hq * d), W["wo"])
+    h2, x2w = L.rmsnorm(xin_all[rows], W["norm2"], cfg.rms_norm_eps, residual=o)
+    gu = gemm(h2, W["wgu"])
+    mlpw = gemm(L.swiglu(gu[:, :inter], gu[:, inter:]), W["wd"])
+    assert norm_rel(got_x2, x2w) <= 2e-2
+    assert norm_rel(got_mlp, mlpw) <= 2e-2
+
+
 def test_decode_steps_match_prefill(ly, gpu):
     """Incremental decode against the reference's generation semantics, which
     recompute the whole prefill per new token and read the last position
@@ -274,6 +355,27 @@ def test_gemv_fused_input_forms_bit_identical(ly, gpu, rows, cols, form):
             assert torch.equal(ro_got, ro_want)
     torch.cuda.synchronize()
     assert got.shape == want.shape == (1, rows)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4104), (37, 4168), (129, 4144)])
+@pytest.mark.parametrize("form", ["bf16", "f32"])
+def test_gemv_fused_uneven_wave_split(ly, gpu, rows, cols, form):
+    """Widths whose 16-byte chunks split unevenly over the four waves of a
+    workgroup, so that the last wave holds fewer chunks than the others (at
+    4104-4168 columns: three waves past one round of chunks, the last within
+    it).  Every wave must take the same loop, whose barriers the row sum
+    crosses; the result is lc_gemv's, bit for bit."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows * 13 + cols)
+    w = _rand_bf16(torch, g, (rows, cols), 0.05)
+    x32 = torch.randn(1, cols, generator=g, device="cuda")
+    x = x32.to(torch.bfloat16)
+    got = ly.gemv_fused(x if form == "bf16" else x32, w)
+    want = ly.linear(x, w)
+    torch.cuda.synchronize()
     assert torch.equal(got, want)
 
 

@@ -703,6 +703,53 @@ def test_ring_c4_shape_reduced(ra, gpu):
         assert norm_rel(_np(a), b) <= BF16_TOL
 
 
+@pytest.mark.parametrize("world,rank,n,hq,hkv,valid,chunked", [
+    (1, 0, 700, 4, 2, None, False),     # the dense replacement: one diagonal pair, GQA, tails
+    (1, 0, 700, 4, 2, None, True),      # the same with a workspace for 256-row chunks only
+    (3, 2, 300, 4, 4, 830, False),      # diagonal shared, two recomputed dQ hops, valid_length
+    (2, 1, 513, 2, 1, None, True),      # chunks of 256 rows plus a 1-row tail chunk
+])
+def test_ring_bwd_shares_ds_on_the_diagonal(ra, gpu, world, rank, n, hq, hkv, valid, chunked):
+    """lc_ring_bwd with the workspace of lc_ring_bwd_ds_workspace_bytes runs the
+    diagonal pair (hop 0 of both reference passes, rs:367-460) as one dS-sharing
+    run; with the base workspace it recomputes the scores in each pass.  Both
+    against the C restatement at the bf16 bar, through the C ABI."""
+    from longctx100m_amd import _lib
+
+    rng = np.random.default_rng(world * 1000 + n + int(chunked))
+    d = 128
+    qs, ks, vs = _rand_shards(gpu, rng, world, n, hq, hkv, d, gpu.bfloat16)
+    gos = [_t(gpu, rng.standard_normal((1, n, hq, d)), gpu.bfloat16) for _ in range(world)]
+    shards = list(zip(qs, ks, vs))
+    fw = [ra.ring_causal_attention_forward_with_stats(shards, r, True, 64, 128, valid)
+          for r in range(world)]
+    outs, ms, ls = (list(x) for x in zip(*fw))
+    _, grads = _oracle_ring(qs, ks, vs, world, hq, hkv, rank=rank, gos=gos, valid_length=valid)
+    lib = _lib.load()
+    desc = _lib.RingDesc(world, rank, 1, n, hq, hkv, d, _lib.LC_DTYPE_BF16, 0, 1, 64, 128,
+                         -1 if valid is None else valid, -1)
+    base = lib.lc_ring_bwd_workspace_bytes(desc)
+    full = lib.lc_ring_bwd_ds_workspace_bytes(desc)
+    per32 = hq * ((n + 31) // 32) * 2048  # dS bytes of one 32-row query tile
+    assert full == base + per32 * ((n + 31) // 32)
+    sizes = [base, base + 8 * per32] if chunked else [base, full]
+    arrs = [_lib.ptr_array([t.data_ptr() for t in ts]) for ts in
+            (qs, ks, vs, outs, [x.contiguous() for x in ms], [x.contiguous() for x in ls], gos)]
+    results = []
+    for ws_bytes in sizes:
+        dq, dk, dv = (gpu.empty_like(x) for x in (qs[rank], ks[rank], ks[rank]))
+        ws = gpu.empty(ws_bytes, dtype=gpu.uint8, device="cuda")
+        _lib.check(lib.lc_ring_bwd(desc, *[a[0] for a in arrs], dq.data_ptr(), dk.data_ptr(),
+                                   dv.data_ptr(), ws.data_ptr(), ws_bytes, None))
+        gpu.cuda.synchronize()
+        for a, e in zip((dq, dk, dv), grads):
+            assert norm_rel(_np(a), e) <= BF16_TOL
+        results.append((dq, dk, dv))
+    # the two paths agree far inside the bar (bf16 outputs; different kernels)
+    for a, b in zip(*results):
+        assert norm_rel(_np(a), _np(b)) <= 8e-3
+
+
 def test_host_pointer_entry_points(gpu):
     """lc_ring_fwd_with_stats_host / lc_ring_bwd_host (the CPU-tensor form a
     candle backend binds) agree with the oracle."""
