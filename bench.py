@@ -88,6 +88,10 @@ def parse():
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the short runs of configs 5, 4 (prefill attention) and the C4 decode "
                          "that follow the headline measurement")
+    ap.add_argument("--kernel-power", action="store_true",
+                    help="run each ring kernel class of configs 2/3 back to back for ~2 s and "
+                         "report its time per launch with the socket power and shader clock "
+                         "(amdsmi) it runs at")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -158,6 +162,47 @@ def cpu_baseline(args, target_s: float):
     }
 
 
+class PowerReader:
+    """Socket power (W) and current shader clock (MHz) of the GPU torch runs on,
+    through amdsmi's read-only metrics query; ``ok`` is False when amdsmi is
+    unavailable or the device cannot be matched by its PCI address."""
+
+    def __init__(self, torch):
+        self.ok, self.cap_w = False, None
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            pr = torch.cuda.get_device_properties(0)
+            bdf = f"{pr.pci_domain_id:04x}:{pr.pci_bus_id:02x}:{pr.pci_device_id:02x}.0"
+            try:
+                self.h = amdsmi.amdsmi_get_processor_handle_from_bdf(bdf)
+            except Exception:  # noqa: BLE001 - fall back to the only GPU amdsmi sees
+                hs = amdsmi.amdsmi_get_processor_handles()
+                if len(hs) != 1:
+                    return
+                self.h = hs[0]
+            self.amdsmi = amdsmi
+            try:
+                cap = amdsmi.amdsmi_get_power_cap_info(self.h).get("power_cap")
+                self.cap_w = round(cap / 1e6, 1) if cap else None  # reported in microwatts
+            except Exception:  # noqa: BLE001
+                pass
+            self.ok = self.read() is not None
+        except Exception:  # noqa: BLE001 - best effort
+            self.ok = False
+
+    def read(self):
+        try:
+            m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.h)
+        except Exception:  # noqa: BLE001
+            return None
+        w, mhz = m.get("current_socket_power"), m.get("current_gfxclk")
+        if not isinstance(w, (int, float)) or w in (0xFFFF, 0xFFFFFFFF):
+            return None
+        return float(w), (float(mhz) if isinstance(mhz, (int, float)) and mhz != 0xFFFF else None)
+
+
 class ClockSampler:
     """Samples the GPU's current shader clock (torch.cuda.clock_rate, read
     through amdsmi) every ``period`` seconds while running, so a bench line
@@ -165,9 +210,11 @@ class ClockSampler:
     several percent under these kernels, and every kernel time scales with it.
     Reports None when the clock cannot be read (no amdsmi access)."""
 
-    def __init__(self, torch, period: float = 0.02):
+    def __init__(self, torch, period: float = 0.02, power: "PowerReader" = None):
         self.torch, self.period = torch, period
         self.samples = []
+        self.power = power if power is not None and power.ok else None
+        self.power_samples = []
         self._stop = threading.Event()
         self._thread = None
 
@@ -183,6 +230,10 @@ class ClockSampler:
             if v is None:
                 return
             self.samples.append(v)
+            if self.power is not None:
+                pw = self.power.read()
+                if pw is not None:
+                    self.power_samples.append(pw[0])
 
     def __enter__(self):
         if self._read() is not None:
@@ -199,6 +250,14 @@ class ClockSampler:
     # rocprofv3 most readings come back at the 158 MHz idle level): they are dropped,
     # and with fewer than half the readings left there is no summary.
     MIN_BUSY_MHZ = 500.0
+
+    def power_summary(self):
+        """Socket power while the timed region ran (W), and the board's cap."""
+        xs = self.power_samples
+        if not xs:
+            return None
+        return {"mean": round(sum(xs) / len(xs), 1), "max": max(xs), "samples": len(xs),
+                "cap": self.power.cap_w}
 
     def summary(self):
         xs = [x for x in self.samples if x >= self.MIN_BUSY_MHZ]
@@ -301,6 +360,67 @@ def long_shard_line(torch, ra, steps: int, warmup: int) -> dict:
 def long_shard(args, torch, ra) -> int:
     line = long_shard_line(torch, ra, max(1, min(args.steps, 2)), max(0, min(args.warmup, 1)))
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def kernel_power(args, torch, ra) -> int:
+    """Socket power and shader clock under each kernel class of one full hop at
+    configs 2/3 (rank 7 of 8: queries at 7 n, keys at 0; bf16, 16 heads, d = 128),
+    each launched back to back for ~2 s: the merging forward; the benched
+    backward pair (dK/dV storing dS, then dQ from dS); the dK/dV kernel alone
+    without dS stores; the recomputing dQ kernel."""
+    n, h, d = args.tokens, args.heads, args.head_dim
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4242)
+    bf = torch.bfloat16
+    randn = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(bf)  # noqa: E731
+    q, k, v, do = (randn(1, n, h, d) for _ in range(4))
+    qp = 7 * n
+    o, m, l = ra.fwd_shard(q, k, v, q_pos0=qp, k_pos0=0)
+    out = torch.empty_like(q)
+    ra.cast(o, out)
+    delta, lse2 = ra.bwd_preprocess(out, do, m, l)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dq, dk, dv = (torch.zeros(1, n, h, d, **f32) for _ in range(3))
+    ws = torch.empty(ra.bwd_shard_workspace_bytes(q, k), dtype=torch.uint8, device=dev)
+    args_b = (q, k, v, do, lse2, delta)
+    unit = 4.0 * n * n * h * d
+    kernels = {
+        "fwd128_kernel<8> (merging full hop)": (unit, lambda: ra.fwd_shard(
+            q, k, v, q_pos0=qp, k_pos0=0, o=o, m=m, l=l, accumulate=True)),
+        "dkdv128_kernel + dqds128_kernel (the benched pair)": (2.5 * unit, lambda: ra.bwd_shard(
+            *args_b, q_pos0=qp, k_pos0=0, dq_acc=dq, dk_acc=dk, dv_acc=dv, workspace=ws)),
+        "dkdv128_kernel without dS stores": (2.0 * unit, lambda: ra.bwd_shard(
+            *args_b, q_pos0=qp, k_pos0=0, dk_acc=dk, dv_acc=dv)),
+        "dq128_kernel (recomputing S and dP)": (1.5 * unit, lambda: ra.bwd_shard(
+            *args_b, q_pos0=qp, k_pos0=0, dq_acc=dq)),
+    }
+    pr = PowerReader(torch)
+    res = {}
+    for name, (flops, fn) in kernels.items():
+        fn()
+        torch.cuda.synchronize()
+        reps, t0 = 0, time.perf_counter()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with ClockSampler(torch, period=0.05, power=pr) as clock:
+            a.record()
+            while time.perf_counter() - t0 < 2.0:
+                for _ in range(4):
+                    fn()
+                    reps += 1
+                torch.cuda.synchronize()
+            b.record()
+            b.synchronize()
+        ms = a.elapsed_time(b) / reps
+        res[name] = {"ms_per_launch": round(ms, 3), "launches": reps,
+                     "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "power_w": clock.power_summary(), "sclk_mhz": clock.summary()}
+        log(f"{name}: {ms:.3f} ms, power {res[name]['power_w']}, clock {res[name]['sclk_mhz']}")
+    print(json.dumps({"metric": "socket power and shader clock per ring kernel class (one full "
+                                "hop, configs 2/3)", "power_cap_w": pr.cap_w if pr.ok else None,
+                      "kernels": res, "box": socket.gethostname()}), flush=True)
     return 0
 
 
@@ -701,6 +821,8 @@ def main() -> int:
         return long_shard(args, torch, ra)
     if args.host_path:
         return host_path(args, torch, ra)
+    if args.kernel_power:
+        return kernel_power(args, torch, ra)
     if args.c4_prefill:
         return c4_prefill(args, torch, ra)
     if args.c4_model:
@@ -751,7 +873,7 @@ def main() -> int:
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
-    with ClockSampler(torch) as clock:
+    with ClockSampler(torch, power=PowerReader(torch)) as clock:
         t_start.record()
         for i in range(args.steps):
             step(True)
@@ -811,6 +933,8 @@ def main() -> int:
                                              if traffic and alg_bytes else None),
                 "ds_exchange_bytes": (2 * n * n * h * 2 if "dqds128" in rl_kernel else 0),
                 "sclk_mhz": sclk,
+                # socket power over the timed region (amdsmi), against the board's cap
+                "power_w": clock.power_summary(),
                 # the same fraction against the peak scaled to the mean sampled shader clock
                 # (the 2516.6 TFLOP/s peak assumes 2.4 GHz; the samples are the firmware's
                 # clock levels, so this is approximate): comparable across boxes
