@@ -14,6 +14,8 @@ bench.py times (longctx100m_amd.rank_step).
   Hkv = 8, rank 3 of 4, forward and backward through the same step with a
   16 GiB dS workspace (query chunks; the full one would be 275 GB), one KV
   head and its 4 query heads checked in full (dK/dV summed over the group).
+* The reference's signatures at configs 2/3 size (lc_ring_fwd_with_stats and
+  lc_ring_bwd, the diagonal pair sharing dS), checked in full for two heads.
 * a 1,000,000-token bf16 shard at rank 1 of 2 (diagonal +
   one full 1M-token KV shard), forward with LSE merge; sampled rows of two
   heads against an fp32 recompute over all visible keys, including the rows
@@ -126,6 +128,64 @@ def test_c2_c3_benched_step_full_size(gpu):
     for b in rs.owners:
         assert torch.isfinite(rs.dk_acc[b]).all() and torch.isfinite(rs.dv_acc[b]).all()
     del rs
+    torch.cuda.empty_cache()
+
+
+def test_c2_reference_signatures_full_size(gpu):
+    """The reference's own signatures at configs 2/3 size, rank 7 of 8:
+    ring_causal_attention_forward_with_stats, then ring_causal_attention_backward
+    (rs:139-233, rs:281-475) through lc_ring_fwd_with_stats and lc_ring_bwd. The
+    backward gets the workspace of lc_ring_bwd_ds_workspace_bytes (32 GiB more),
+    so the diagonal pair (hop 0 of both passes) shares dS; the other 7 hops of
+    pass 2 recompute dQ.  Heads 0 and 11 in full: the output, dQ of every row,
+    and dK/dV of the rank's own shard (from its own queries only: no later rank
+    exists)."""
+    torch = gpu
+    from longctx100m_amd import _lib
+    from longctx100m_amd import ring_attention as ra
+
+    world, rank, n, h, d = 8, 7, 32768, 16, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(777)
+    rnd = lambda *s: torch.randn(*s, generator=gen, device=dev).to(torch.bfloat16)  # noqa: E731
+    qs = [rnd(1, n, h, d) for _ in range(world)]
+    ks = [rnd(1, n, h, d) for _ in range(world)]
+    vs = [rnd(1, n, h, d) for _ in range(world)]
+    go = rnd(1, n, h, d)
+    shards = list(zip(qs, ks, vs))
+    desc = ra._ring_desc(shards, rank, True, 64, 128, None, None, False)
+    lib = _lib.load()
+    extra = lib.lc_ring_bwd_ds_workspace_bytes(desc) - lib.lc_ring_bwd_workspace_bytes(desc)
+    assert extra == 32 << 30
+    print(f"fullsize reference signatures: world={world} rank={rank} n={n} H={h} d={d} bf16, "
+          f"dS workspace {extra / 2**30:.1f} GiB", flush=True)
+    out, m, l = ra.ring_causal_attention_forward_with_stats(shards, rank)
+    # only this rank's forward results and upstream gradient enter its backward (every
+    # pass-1 pair of an earlier query owner is masked for the last rank's keys)
+    dq, dk, dv = ra.ring_causal_attention_backward(shards, rank, [out] * world, [m] * world,
+                                                   [l] * world, [go] * world)
+    torch.cuda.synchronize()
+    scale = d ** -0.5
+    for hh in (0, 11):
+        kall = torch.cat([x[0, :, hh] for x in ks], 0).float()
+        vall = torch.cat([x[0, :, hh] for x in vs], 0).float()
+        eo, em, el, edq, edk, edv = _head_reference(torch, qs[rank][0, :, hh].float(), kall,
+                                                    vall, go[0, :, hh].float(), rank * n, scale)
+        own = slice(rank * n, (rank + 1) * n)
+        errs = {"out": _nrel(out[0, :, hh].float(), eo),
+                "m": float(((m[0, hh, :, 0] - em).abs() / em.abs().clamp(min=1.0)).max()),
+                "l": float(((l[0, hh, :, 0] - el).abs() / el).max()),
+                "dq": _nrel(dq[0, :, hh].float(), edq),
+                "dk": _nrel(dk[0, :, hh].float(), edk[own]),
+                "dv": _nrel(dv[0, :, hh].float(), edv[own])}
+        print(f"fullsize reference signatures head {hh}: " +
+              ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+        bad = {k: v for k, v in errs.items()
+               if not v <= {"m": 1e-4, "l": 1e-3}.get(k, BF16_TOL)}
+        assert not bad, f"head {hh}: {bad}"
+        del kall, vall, eo, edq, edk, edv
+    del out, m, l, dq, dk, dv
     torch.cuda.empty_cache()
 
 
