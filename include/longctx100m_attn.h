@@ -233,8 +233,8 @@ int lc_ring_fwd_with_stats(const lc_ring_desc_t* desc, const void* const* qs,
  * dk, dv [B,n,Hkv,D] in dtype.  Pass 1 uses query positions owner*n + i and
  * pass 2 uses q_position_start (default rank*n) + i, as the reference does
  * (rs:377, rs:419).  The workspace needs lc_ring_bwd_workspace_bytes; with
- * more (up to lc_ring_bwd_ds_workspace_bytes), the diagonal pair's dK/dV and
- * dQ come from one dS-sharing run (the dK/dV kernel stores dS in the extra
+ * more (up to lc_ring_bwd_ds_workspace_bytes) and 256-byte alignment, the
+ * diagonal pair's dK/dV and dQ come from one dS-sharing run (the dK/dV kernel stores dS in the extra
  * bytes, the dQ kernel reads it) instead of a recomputing run of each, with
  * the same results up to fp32 summation order.  The host form below uses
  * the larger workspace when it can allocate it. */

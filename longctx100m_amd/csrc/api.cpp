@@ -639,7 +639,8 @@ int lc_ring_bwd(const lc_ring_desc_t* d, const void* const* qs, const void* cons
   int64_t ds_chunk = 0;
   uint16_t* ds = nullptr;
   if (q_pos0 == (int64_t)r * n && pair_active(pd) &&
-      ds_path(pd, qs[r], ks[r], vs[r], grad_outs[r]) && workspace_bytes > bwd_ws_bytes(d)) {
+      ds_path(pd, qs[r], ks[r], vs[r], grad_outs[r]) && workspace_bytes > bwd_ws_bytes(d) &&
+      (reinterpret_cast<uintptr_t>(workspace) & 255) == 0) {  // dS blocks as in _ws
     ds = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + bwd_ws_bytes(d));
     ds_chunk = ds_chunk_rows(pd, workspace_bytes - bwd_ws_bytes(d));
   }
