@@ -9,6 +9,11 @@ lib.rs:16-19):
 * ring_causal_attention_backward           rs:281-475
 * reference_causal_attention               rs:237-270
 
+and the Python module's process-group entry (src/longctx100m/ring_attention.py):
+
+* ring_causal_attention(q, k, v, *, group, ...)  py:176-191, with the autograd
+  of _RingCausalAttention (py:194-255): what model.py:254-265 calls
+
 ``shards`` is every rank's (q, k, v) triple in rank order, each a contiguous
 ``[B, local_tokens, H, D]`` tensor on the GPU; the ring is emulated on one GPU
 as an ordered loop over the KV shards held in HBM.  Unlike the reference,
@@ -395,3 +400,96 @@ class RingCausalAttention(torch.autograd.Function):
                                                     ctx.ls, grad_outs, ctx.causal, 64, 128,
                                                     ctx.valid_length, ctx.q_position_start)
         return dq, dk, dv, None, None, None, None, None
+
+
+# ------------------------------------------------- the Python module's entry --
+
+def ring_causal_attention(q, k, v, *, group=None, causal=True, block_q=64, block_k=128,
+                          valid_length=None, q_position_start=None):
+    """Exact ring attention over a torch.distributed process group with the
+    activation-recomputing backward: the signature of
+    ring_causal_attention (src/longctx100m/ring_attention.py:176-191), which
+    model.py:254-265 calls with this rank's [B, local_tokens, H, D] shards.
+
+    Each rank gathers the group's K and V shards once (one all_gather each;
+    the reference rotates them hop by hop) and runs the ring over them in HBM.
+    The backward gathers Q, dO, O, m and l the same way for the reference's
+    pass 1 (each rank differentiates its own K/V against every query owner)
+    and returns this rank's (dq, dk, dv).  With one rank and
+    ``q_position_start`` set, the backward takes the reference's decode path
+    (py:226-239).  Tensors must be on the GPU (the kernels have no CPU form),
+    with an NCCL (RCCL) group as the reference requires for CUDA tensors."""
+    return _GroupRingAttention.apply(q, k, v, group, causal, block_q, block_k, valid_length,
+                                     q_position_start)
+
+
+def _group_checks(q, k, v, group, block_q, block_k, valid_length):
+    """The reference's argument checks (py:78-101), in its order and texts."""
+    import torch.distributed as dist
+
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, v must have shape [batch, tokens, heads, head_dim]")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v shard shapes must match")
+    if block_q <= 0 or block_k <= 0:
+        raise ValueError("block_q and block_k must be positive")
+    if q.device.type != "cuda":
+        raise ValueError("ring attention on this backend requires CUDA (HIP) tensors")
+    if not dist.is_available() or not dist.is_initialized():
+        raise RuntimeError("torch.distributed must be initialized")
+    if not str(dist.get_backend(group)).lower().endswith("nccl"):
+        raise RuntimeError("CUDA ring attention requires an NCCL process group")
+    world, rank = dist.get_world_size(group), dist.get_rank(group)
+    if world < 1:
+        raise RuntimeError("invalid distributed group")
+    if q.shape[1] == 0:
+        raise ValueError("local_tokens must be positive")
+    if valid_length is not None and not 0 < valid_length <= world * q.shape[1]:
+        raise ValueError("valid_length must be within the padded distributed sequence")
+    return world, rank
+
+
+def _gather(x, world, group):
+    """Every rank's copy of x, in rank order (one all_gather)."""
+    import torch.distributed as dist
+
+    x = x.contiguous()
+    if world == 1:
+        return [x]
+    out = [torch.empty_like(x) for _ in range(world)]
+    dist.all_gather(out, x, group=group)
+    return out
+
+
+class _GroupRingAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, group, causal, block_q, block_k, valid_length, q_position_start):
+        world, rank = _group_checks(q, k, v, group, block_q, block_k, valid_length)
+        with torch.no_grad():
+            ks, vs = _gather(k, world, group), _gather(v, world, group)
+            shards = [(q.contiguous(), kk, vv) for kk, vv in zip(ks, vs)]
+            out, m, l = ring_causal_attention_forward_with_stats(
+                shards, rank, causal, block_q, block_k, valid_length, q_position_start)
+        ctx.group, ctx.world, ctx.rank = group, world, rank
+        ctx.causal, ctx.block_q, ctx.block_k = causal, block_q, block_k
+        ctx.valid_length, ctx.q_position_start = valid_length, q_position_start
+        ctx.save_for_backward(q, k, v, out, m, l)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, m, l = ctx.saved_tensors
+        none6 = (None,) * 6
+        if ctx.q_position_start is not None and ctx.world == 1:
+            return (*local_decode_backward(q, k, v, out, m, l, grad_out.contiguous(),
+                                           causal=ctx.causal,
+                                           q_position_start=ctx.q_position_start,
+                                           valid_length=ctx.valid_length), *none6)
+        w, g = ctx.world, ctx.group
+        qs, ks, vs = _gather(q, w, g), _gather(k, w, g), _gather(v, w, g)
+        outs, gos = _gather(out, w, g), _gather(grad_out, w, g)
+        ms, ls = _gather(m, w, g), _gather(l, w, g)
+        dq, dk, dv = ring_causal_attention_backward(
+            list(zip(qs, ks, vs)), ctx.rank, outs, ms, ls, gos, ctx.causal, ctx.block_q,
+            ctx.block_k, ctx.valid_length, ctx.q_position_start)
+        return (dq, dk, dv, *none6)

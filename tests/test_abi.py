@@ -328,3 +328,22 @@ def test_rmsnorm_residual_out_stride_checked(lib):
                         fake, 64, None)
     assert rc == _lib.LC_ERR_INVALID
     assert lib.lc_last_error().decode() == "row strides must be >= cols and multiples of 8 elements"
+
+
+def test_python_signature_argument_checks():
+    """ring_causal_attention(q, k, v, *, group, ...) checks its arguments as the
+    reference does (src/longctx100m/ring_attention.py:78-101), before any device
+    work; this backend has no CPU kernels, so CPU tensors are refused."""
+    import torch
+
+    from longctx100m_amd import ring_attention as ra
+
+    x = torch.zeros(1, 8, 2, 4)
+    with pytest.raises(ValueError, match=re.escape("q, k, v must have shape [batch, tokens, heads, head_dim]")):
+        ra.ring_causal_attention(x[0], x, x)
+    with pytest.raises(ValueError, match="q, k, v shard shapes must match"):
+        ra.ring_causal_attention(x, x[:, :4], x)
+    with pytest.raises(ValueError, match="block_q and block_k must be positive"):
+        ra.ring_causal_attention(x, x, x, block_q=0)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        ra.ring_causal_attention(x, x, x)

@@ -998,3 +998,55 @@ def test_random_shapes_shared_ds_partial_workspace(ra, gpu, case):
     assert norm_rel(_np(dq), edq) <= BF16_TOL
     assert norm_rel(_np(dk), edk) <= BF16_TOL
     assert norm_rel(_np(dv), edv) <= BF16_TOL
+
+
+@pytest.fixture
+def one_rank_nccl_group(gpu):
+    """A one-process NCCL (RCCL) group on this GPU, as the reference's Python entry
+    requires for CUDA tensors (py:88-92); nothing is communicated."""
+    import socket
+
+    import torch.distributed as dist
+
+    assert not dist.is_initialized()
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        port = s.getsockname()[1]
+    dist.init_process_group("nccl", init_method=f"tcp://127.0.0.1:{port}", rank=0, world_size=1)
+    try:
+        yield dist.group.WORLD
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("dtype_name,qps,valid_length", [("bfloat16", None, None),
+                                                         ("float32", None, 250),
+                                                         ("bfloat16", 500, None)])
+def test_python_signature_in_a_group(ra, gpu, one_rank_nccl_group, dtype_name, qps,
+                                     valid_length):
+    """ring_causal_attention(q, k, v, *, group, ...) with the Python reference's
+    signature (src/longctx100m/ring_attention.py:176-191), called as model.py:254-265
+    calls it: autograd forward and backward on a one-rank NCCL group, against the fp64
+    dense closed form (with q_position_start, the reference's decode backward)."""
+    d, n, h = 128, 300, 4
+    dtype = getattr(gpu, dtype_name)
+    rng = np.random.default_rng(zlib.crc32(repr((dtype_name, qps, valid_length)).encode()))
+    qs, ks, vs = _rand_shards(gpu, rng, 1, n, h, h, d, dtype)
+    q = qs[0].clone().requires_grad_()
+    k = ks[0].clone().requires_grad_()
+    v = vs[0].clone().requires_grad_()
+    out = ra.ring_causal_attention(q, k, v, group=one_rank_nccl_group, valid_length=valid_length,
+                                   q_position_start=qps)
+    go = _t(gpu, rng.standard_normal((1, n, h, d)), dtype)
+    out.backward(go)
+    gpu.cuda.synchronize()
+    tol = BF16_TOL if dtype_name == "bfloat16" else FP32_TOL
+    qp = 0 if qps is None else qps
+    eo = dense.attention_fwd(_np(qs[0]), _np(ks[0]), _np(vs[0]), q_pos0=qp, k_pos0=0,
+                             valid_length=valid_length)[0]
+    assert norm_rel(_np(out), eo) <= tol
+    oref = _np(out) if dtype_name == "bfloat16" else eo  # delta uses the cast output
+    edq, edk, edv = dense.attention_bwd(_np(qs[0]), _np(ks[0]), _np(vs[0]), _np(go), q_pos0=qp,
+                                        k_pos0=0, valid_length=valid_length, out=oref)
+    for a, e in ((q.grad, edq), (k.grad, edk), (v.grad, edv)):
+        assert norm_rel(_np(a), e) <= tol
