@@ -92,6 +92,10 @@ def parse():
                     help="run each ring kernel class of configs 2/3 back to back for ~2 s and "
                          "report its time per launch with the socket power and shader clock "
                          "(amdsmi) it runs at")
+    ap.add_argument("--cpu-shard", action="store_true",
+                    help="only time the CPU baseline at the workload's own shard size (one head, "
+                         "world 2 rank 1: one full hop and the diagonal of --tokens-token shards, "
+                         "about 45 s on 16 threads) and print its JSON line; no GPU work")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes)")
@@ -119,7 +123,7 @@ def cpu_baseline(args, target_s: float):
 
     world, rank, d = args.world, args.rank, args.head_dim
 
-    def run(ns):
+    def run(ns, world=world, rank=rank):
         rng = np.random.default_rng(99)
         mk = lambda: rng.standard_normal((1, ns, 1, d)).astype(np.float32)  # noqa: E731
         qs = [mk() for _ in range(world)]
@@ -135,8 +139,30 @@ def cpu_baseline(args, target_s: float):
         ls = [np.ones_like(l) for _ in range(world)]
         gos = [np.zeros_like(go) for _ in range(world)]
         outs[rank], ms[rank], ls[rank], gos[rank] = out, m, l, go
+        t1 = time.perf_counter()
+        log(f"cpu baseline: {ns}-token shards, world {world} rank {rank}: forward {t1 - t0:.1f} s")
         oring.ring_bwd(qs, ks, vs, outs, ms, ls, gos, rank)
-        return time.perf_counter() - t0
+        t2 = time.perf_counter()
+        log(f"cpu baseline: backward {t2 - t1:.1f} s")
+        return t2 - t0
+
+    if args.cpu_shard:
+        # the workload's own shard size on the smallest ring that holds both hop kinds
+        ns, world, rank = args.tokens, 2, 1
+        t = run(ns, world, rank)
+        flops = 3.5 * 4.0 * ns * ns * d * 1.5
+        return {
+            "value": round(flops / t / 1e12, 6),
+            "unit": "TFLOP/s",
+            "cores": oring.num_threads(),
+            "cpu_model": cpu_model(),
+            "kind": "port",
+            "sample": (f"C restatement of the reference algorithm (fp32, block_q=64, "
+                       f"block_k=128, two-pass backward), 1 head, world 2 rank 1 (one full hop "
+                       f"and the diagonal), {ns}-token shards, d={d}: fwd+bwd "
+                       f"{flops / 1e9:.1f} GFLOP in {t:.2f} s"),
+            "seconds": round(t, 3),
+        }
 
     ns = 256
     t = run(ns)
@@ -813,6 +839,15 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         log("copy calibration: 3 copies of 1 GiB (1048576 KiB read + written each)")
+        return 0
+
+    if args.cpu_shard:
+        cpu = cpu_baseline(args, 0.0)
+        # configs 2+3 count 7.5 full hops of forward per head, 3.5x that with the backward
+        full = 3.5 * 4.0 * args.tokens ** 2 * args.head_dim * (args.rank + 0.5) * args.heads
+        cpu["extrapolated_full_config_s"] = round(full / (cpu["value"] * 1e12), 1)
+        print(json.dumps({"metric": "cpu baseline at the workload's shard size",
+                          "cpu_baseline": cpu}), flush=True)
         return 0
 
     from longctx100m_amd import ring_attention as ra
