@@ -738,12 +738,17 @@ def test_ring_bwd_shares_ds_on_the_diagonal(ra, gpu, world, rank, n, hq, hkv, va
     results = []
     for ws_bytes in sizes:
         dq, dk, dv = (gpu.empty_like(x) for x in (qs[rank], ks[rank], ks[rank]))
-        ws = gpu.empty(ws_bytes, dtype=gpu.uint8, device="cuda")
+        ws = gpu.full((ws_bytes,), 0xFF, dtype=gpu.uint8, device="cuda")  # bf16 NaN pattern
         _lib.check(lib.lc_ring_bwd(desc, *[a[0] for a in arrs], dq.data_ptr(), dk.data_ptr(),
                                    dv.data_ptr(), ws.data_ptr(), ws_bytes, None))
         gpu.cuda.synchronize()
         for a, e in zip((dq, dk, dv), grads):
             assert norm_rel(_np(a), e) <= BF16_TOL
+        if ws_bytes > base:
+            # the shared run stored the diagonal's dS past the base workspace (about half
+            # of its blocks: the causal triangle), so the dS path did run
+            written = float((ws[base:] != 0xFF).float().mean())
+            assert written > 0.25, written
         results.append((dq, dk, dv))
     # the two paths agree far inside the bar (bf16 outputs; different kernels)
     for a, b in zip(*results):
