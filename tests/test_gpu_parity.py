@@ -310,6 +310,11 @@ def test_bwd_shard_shared_ds(ra, gpu, case):
         ra.bwd_shard(q, k, v, do, lse2, delta, dq_acc=dq, dk_acc=dk, dv_acc=dv, workspace=w, **kw)
         grads.append((_np(dq), _np(dk), _np(dv)))
     gpu.cuda.synchronize()
+    # the dS path ran (it overwrote part of the NaN workspace) exactly when the workspace
+    # holds 256 query rows or the whole shard; the 1% case falls back to recomputing
+    per_tile = b * hq * -(-nk // 32) * 2048
+    rows = ws.numel() * 2 // per_tile * 32
+    assert bool(gpu.isnan(ws).all()) == (rows < 256 and rows < nq)
     (dq, dk, dv), (rdq, rdk, rdv) = grads
     tiles = full // (b * hq * -(-nk // 32) * 2048)  # 32-row query tiles of the full workspace
     chunked = 8 <= int(full * frac) // (full // tiles) < -(-nq // 32)
